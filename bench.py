@@ -1,0 +1,199 @@
+"""Benchmark of the attention hot path on one MI355X.
+
+Headline (`value`): paged decode attention at cfg2 (B=32, ctx ~ U[128, 4096],
+24/8 heads, D=128, 16-token pages, shuffled block tables) in algorithmic HBM
+GB/s: every K/V byte once, q and out once, the block-table entries used.
+One "step" = one paged_attention_decode call over the whole batch, inputs
+resident in HBM.  Timed with HIP events on the launch stream over K steps.
+
+Extra fields on the same JSON line:
+  prefill   cfg3 causal prefill (S=2048, 24/8 heads): algorithmic TFLOP/s
+            (2 * D * Hq * S * (S+1)) and fraction of dense fp16 MFMA peak.
+  splitk    cfg4 long-context decode (B=8, ctx 32768): GB/s.
+  model     Llama-3.2-3B random-init graph-replayed decode tok/s (when built).
+  cpu_baseline  the CPU oracle on the same cfg2 inputs, on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor spec
+FP16_DENSE_TFLOPS = 2500.0     # MI355X dense fp16 MFMA, vendor spec
+METRIC = "decode-attn HBM GB/s (% peak); prefill-attn TFLOPS (% MFMA); 3B decode tok/s"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_gpu(fn, steps: int, warmup: int) -> float:
+    """Average ms per call of fn() with HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        fn()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def cpu_info() -> dict:
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "torch": torch.__version__}
+
+
+def bench_decode(case, dev, steps, warmup):
+    import my_cuda_engine_cpp as ops
+    q = case.query.to(dev)
+    kc, vc = case.key_cache.to(dev), case.value_cache.to(dev)
+    bt, cl = case.block_tables.to(dev), case.context_lens.to(dev)
+    fn = lambda: ops.paged_attention_decode(q, kc, vc, bt, cl, case.max_blocks,
+                                            case.block_size, case.scale)
+    ms = time_gpu(fn, steps, warmup)
+    nbytes = case.algorithmic_bytes()
+    return ms, nbytes, nbytes / (ms * 1e-3) / 1e9
+
+
+def bench_prefill(case, dev, steps, warmup):
+    import my_cuda_engine_cpp as ops
+    q, k, v = case.query.to(dev), case.key.to(dev), case.value.to(dev)
+    fn = lambda: ops.prefill_attention(q, k, v, case.scale)
+    ms = time_gpu(fn, steps, warmup)
+    flops = case.algorithmic_flops()
+    return ms, flops, flops / (ms * 1e-3) / 1e12
+
+
+def cpu_baseline_decode(case) -> dict:
+    """The CPU oracle (fp32, torch on this host's cores) on the same inputs."""
+    from oracle.ops_ref import decode_attention_ref
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    args = (case.query, case.key_cache, case.value_cache, case.block_tables,
+            case.context_lens, case.scale)
+    for _ in range(2):
+        decode_attention_ref(*args)
+    times = []
+    t_end = time.perf_counter() + 20.0
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        decode_attention_ref(*args)
+        times.append(time.perf_counter() - t0)
+        if len(times) >= 5 and time.perf_counter() > t_end:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    gbs = case.algorithmic_bytes() / med / 1e9
+    info = cpu_info()
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": n, "kind": "port",
+            "sample": f"full cfg2 batch (32 seqs, {int(case.context_lens.sum())} tokens), "
+                      f"fp32 torch oracle, median of {len(times)} runs after 2 warmups, "
+                      f"{med * 1e3:.1f} ms/run; {info['cpu_model']}; torch {info['torch']}"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=["decode", "prefill", "splitk"], default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
+              "supported (the hot path's multi-GPU sharding is a design note, not built)",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from mycustomcudaengine_amd import _lib
+    _lib.load()
+    from oracle.inputs import cfg2_decode, cfg3_prefill, cfg4_decode
+
+    dev = torch.device("cuda:0")
+    result = {}
+    log("generating cfg2 inputs")
+    case2 = cfg2_decode()
+    ms, nbytes, gbs = bench_decode(case2, dev, args.steps, args.warmup)
+    log(f"cfg2 decode: {ms * 1e3:.1f} us/step, {gbs:.1f} GB/s")
+    result["decode"] = (ms, nbytes, gbs)
+
+    extra = {}
+    if args.only in (None, "prefill"):
+        log("cfg3 prefill")
+        case3 = cfg3_prefill()
+        pms, flops, tfs = bench_prefill(case3, dev, max(20, args.steps // 4), 5)
+        log(f"cfg3 prefill: {pms * 1e3:.1f} us, {tfs:.1f} TFLOP/s")
+        extra["prefill"] = {"workload": "cfg3 causal prefill B=1 S=2048 24/8 heads D=128 fp16",
+                            "us": round(pms * 1e3, 2), "flop": flops,
+                            "tflops": round(tfs, 2),
+                            "frac_of_fp16_dense_peak": round(tfs / FP16_DENSE_TFLOPS, 4)}
+        del case3
+    if args.only in (None, "splitk"):
+        log("generating cfg4 inputs")
+        case4 = cfg4_decode()
+        kms, kbytes, kgbs = bench_decode(case4, dev, max(20, args.steps // 4), 5)
+        log(f"cfg4 split-K decode: {kms * 1e3:.1f} us, {kgbs:.1f} GB/s")
+        extra["splitk"] = {"workload": "cfg4 paged decode B=8 ctx=32768 24/8 heads D=128",
+                           "us": round(kms * 1e3, 2), "bytes": kbytes,
+                           "gbs": round(kgbs, 1), "frac_of_hbm_peak": round(kgbs / HBM_PEAK_GBS, 4)}
+        del case4
+        torch.cuda.empty_cache()
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (oracle on host cores)")
+        cpu = cpu_baseline_decode(case2)
+        log(f"CPU baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
+
+    ms, nbytes, gbs = result["decode"]
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "cfg2 paged decode attention: B=32, ctx~U[128,4096] (seed 43), "
+                               "24 Q / 8 KV heads, D=128, 16-token pages, shuffled tables",
+                   "batch": 32, "tokens": int(case2.context_lens.sum()),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        **extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,165 @@
+/*
+ * mce_abi.h -- C ABI of libmce.so, the gfx950 (MI355X) kernels behind the
+ * `my_cuda_engine_cpp` op surface.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, element counts / strides (in elements) and a
+ *     HIP stream handle passed as `void*` (a hipStream_t; NULL = legacy stream);
+ *   - validates its arguments on the host and returns MCE_OK (0) or a nonzero
+ *     MCE_ERR_* code, with a message available from mce_last_error();
+ *   - launches asynchronously on `stream`: it never synchronises, never reads
+ *     device memory on the host and never allocates device memory, so it may be
+ *     recorded by hipStreamBeginCapture / torch.cuda.graph;
+ *   - checks hipGetLastError() after its launches.
+ *
+ * dtype codes: MCE_F16 (IEEE half) and MCE_BF16 (bfloat16).  Index tensors are
+ * int32, RoPE tables are fp32, as in the reference.
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   csrc/bindings.cpp:4-19,22-29   pybind op surface `my_cuda_engine_cpp`
+ */
+#ifndef MCE_ABI_H
+#define MCE_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__) || defined(__clang__)
+#define MCE_API __attribute__((visibility("default")))
+#else
+#define MCE_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MCE_OK = 0,
+  MCE_ERR_INVALID = 1,     /* bad pointer / shape / stride / value */
+  MCE_ERR_UNSUPPORTED = 2, /* valid request this build has no kernel for */
+  MCE_ERR_LAUNCH = 3,      /* the HIP runtime rejected a launch */
+  MCE_ERR_WORKSPACE = 4    /* workspace missing or smaller than required */
+};
+
+enum { MCE_F16 = 0, MCE_BF16 = 1 };
+
+/* Message of the last failed call on this host thread ("" if none). */
+MCE_API const char *mce_last_error(void);
+
+/* ABI version (major * 100 + minor). */
+MCE_API int mce_abi_version(void);
+
+/*
+ * Fused RMSNorm: out[r, :] = x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * w, with
+ * fp32 accumulation and one rounding to the storage type.
+ * Replaces rmsnorm_cuda (csrc/kernels/rmsnorm.cu:110-130; binding
+ * csrc/bindings.cpp:4-5,23).  Rows are `row_stride` elements apart; the last
+ * dimension is contiguous.  Any hidden size >= 1 is accepted.
+ */
+MCE_API int mce_rmsnorm(int dtype, const void *input, const void *weight, void *output,
+                int64_t rows, int64_t hidden, int64_t in_row_stride,
+                int64_t out_row_stride, float eps, void *stream);
+
+/*
+ * Fused SwiGLU: out[t, j] = silu(gate_up[t, j]) * gate_up[t, I + j], j < I,
+ * silu(x) = x / (1 + exp(-x)).  `inter` is I (half the input's last dim).
+ * Replaces swiglu_cuda (csrc/kernels/swiglu.cu:29-52; binding
+ * csrc/bindings.cpp:6,24).  Computes every row (the reference's guard at
+ * swiglu.cu:13 writes only rows 0-1).
+ */
+MCE_API int mce_swiglu(int dtype, const void *gate_up, void *output, int64_t rows,
+               int64_t inter, int64_t in_row_stride, int64_t out_row_stride,
+               void *stream);
+
+/*
+ * Paged KV store: for each token n with s = slot_mapping[n] >= 0,
+ *   key_cache[s / block_size, s % block_size, h, :]   = key[n, h, :]
+ *   value_cache[s / block_size, s % block_size, h, :] = value[n, h, :]
+ * Caches are contiguous [num_blocks, block_size, num_kv_heads, head_dim].
+ * key/value rows are addressed n * *_stride_tok + h * *_stride_head (the last
+ * dimension contiguous).  Slots >= num_blocks * block_size are skipped.
+ * Replaces paged_kv_store_cuda (csrc/kernels/paged_kv.cu:45-69; binding
+ * csrc/bindings.cpp:7,25), which hard-codes block_size 16 (paged_kv.cu:22).
+ */
+MCE_API int mce_paged_kv_store(int dtype, const void *key, const void *value,
+                       void *key_cache, void *value_cache,
+                       const int32_t *slot_mapping, int64_t num_tokens,
+                       int num_kv_heads, int head_dim, int block_size,
+                       int64_t num_blocks, int64_t key_stride_tok,
+                       int64_t key_stride_head, int64_t value_stride_tok,
+                       int64_t value_stride_head, void *stream);
+
+/*
+ * Workspace bytes mce_paged_attention_decode needs for these dimensions
+ * (split-K partial softmax state).  Depends only on host-known sizes.
+ */
+MCE_API size_t mce_paged_attention_decode_workspace_size(int batch, int num_heads,
+                                                 int max_blocks_per_seq,
+                                                 int block_size);
+
+/*
+ * Paged decode attention (one query token per sequence), GQA:
+ *   out[b, h, :] = sum_{t < ctx_b} softmax_t(scale * q[b,h] . k_t) v_t
+ * with k_t/v_t at cache[block_tables[b, t / block_size], t % block_size,
+ * h / (num_heads / num_kv_heads), :].  query/out are contiguous
+ * [batch, num_heads, head_dim]; caches contiguous
+ * [num_blocks, block_size, num_kv_heads, head_dim]; block_tables int32
+ * [batch, max_blocks_per_seq]; context_lens int32 [batch].
+ * Rows with ctx <= 0 are written as zeros.  ctx is clamped to
+ * max_blocks_per_seq * block_size; block ids outside [0, num_blocks) are
+ * clamped into range (the reference reads out of bounds there).
+ * head_dim must be 128, block_size a power of two in [8, 256],
+ * num_heads / num_kv_heads in [1, 8].
+ * Replaces paged_attention_decode_cuda (csrc/kernels/flash_attn_paged.cu:
+ * 144-168; binding csrc/bindings.cpp:8,26).
+ */
+MCE_API int mce_paged_attention_decode(int dtype, const void *query,
+                               const void *key_cache, const void *value_cache,
+                               const int32_t *block_tables,
+                               const int32_t *context_lens, void *output,
+                               int batch, int num_heads, int num_kv_heads,
+                               int head_dim, int max_blocks_per_seq,
+                               int block_size, int64_t num_blocks, float scale,
+                               void *workspace, size_t workspace_bytes,
+                               void *stream);
+
+/*
+ * In-place rotary embedding (half-split / rotate_half form), i < head_dim/2:
+ *   (x_i, x_{i+D/2}) <- (x_i c - x_{i+D/2} s, x_i s + x_{i+D/2} c),
+ *   c = cos_table[pos, i], s = sin_table[pos, i], pos = positions[token].
+ * query is [batch, seq, num_heads, head_dim], key [batch, seq, num_kv_heads,
+ * head_dim] (key may be NULL), both with arbitrary strides except a
+ * contiguous last dimension; positions int32 [batch * seq] (contiguous);
+ * tables fp32 [table_rows, head_dim / 2] contiguous.  Tokens whose position
+ * is outside [0, table_rows) are left unrotated.
+ * Replaces rope_inplace_cuda (csrc/kernels/rope.cu:64-99; binding
+ * csrc/bindings.cpp:9-13,27).
+ */
+MCE_API int mce_rope_inplace(int dtype, void *query, void *key, const float *cos_table,
+                     const float *sin_table, const int32_t *positions,
+                     int batch, int seq_len, int num_heads, int num_kv_heads,
+                     int head_dim, int64_t table_rows, int64_t q_stride_b,
+                     int64_t q_stride_s, int64_t q_stride_h,
+                     int64_t k_stride_b, int64_t k_stride_s,
+                     int64_t k_stride_h, void *stream);
+
+/*
+ * Causal prefill attention over contiguous Q/K/V, GQA:
+ *   out[b, s, h, :] = sum_{t <= s} softmax_t(scale * q[b,s,h] . k[b,t,g]) v[b,t,g]
+ * with g = h / (num_heads / num_kv_heads).  query/out contiguous
+ * [batch, seq, num_heads, head_dim]; key/value contiguous
+ * [batch, seq, num_kv_heads, head_dim].  head_dim must be 128.
+ * Replaces prefill_attention_cuda (csrc/kernels/prefill_attention.cu:271-309;
+ * binding csrc/bindings.cpp:14-19,28).
+ */
+MCE_API int mce_prefill_attention(int dtype, const void *query, const void *key,
+                          const void *value, void *output, int batch,
+                          int seq_len, int num_heads, int num_kv_heads,
+                          int head_dim, float scale, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MCE_ABI_H */

@@ -1,0 +1,451 @@
+// Bandwidth-bound fused ops: RMSNorm, SwiGLU, paged KV store, in-place RoPE.
+//
+// All four are HBM-bound streaming kernels.  Each uses 16-byte global accesses
+// (8 x 16-bit values per lane) where the row length and alignment allow, and a
+// scalar fallback otherwise; fp32 arithmetic, one rounding to storage type.
+#include "mce_common.h"
+
+namespace mce {
+
+// =========================================================================
+// RMSNorm  (reference: csrc/kernels/rmsnorm.cu:35-108)
+//
+// One wave per row (4 rows per 256-thread workgroup).  The row stays in
+// registers between the sum-of-squares pass and the scaling pass, so every
+// input byte is read once: VPT 16-byte vectors per lane cover rows up to
+// 512 * VPT elements.  Rows longer than that (or not 16-byte aligned) take
+// the two-pass kernel, whose second read hits L2.
+// =========================================================================
+template <class T, int VPT>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(
+    const uint16_t *__restrict__ x, const uint16_t *__restrict__ w,
+    uint16_t *__restrict__ y, int64_t rows, int hidden, int64_t in_stride,
+    int64_t out_stride, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nvec = hidden >> 3;  // 8 elements per 16-byte vector
+  const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + row * in_stride);
+  const u32x4 *wr = reinterpret_cast<const u32x4 *>(w);
+  u32x4 v[VPT];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    int idx = lane + i * 64;
+    if (idx < nvec) {
+      v[i] = xr[idx];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float a = T::lo(v[i][k]), b = T::hi(v[i][k]);
+        ss += a * a + b * b;
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
+  u32x4 *yr = reinterpret_cast<u32x4 *>(y + row * out_stride);
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    int idx = lane + i * 64;
+    if (idx < nvec) {
+      u32x4 wv = wr[idx];
+      u32x4 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float a = T::lo(v[i][k]) * (inv * T::lo(wv[k]));
+        float b = T::hi(v[i][k]) * (inv * T::hi(wv[k]));
+        o[k] = pack2<T>(a, b);
+      }
+      yr[idx] = o;
+    }
+  }
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void rmsnorm_generic_kernel(
+    const uint16_t *__restrict__ x, const uint16_t *__restrict__ w,
+    uint16_t *__restrict__ y, int64_t rows, int hidden, int64_t in_stride,
+    int64_t out_stride, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const uint16_t *xr = x + row * in_stride;
+  float ss = 0.f;
+  for (int i = lane; i < hidden; i += 64) {
+    float a = T::lo(xr[i]);
+    ss += a * a;
+  }
+  ss = wave_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
+  uint16_t *yr = y + row * out_stride;
+  for (int i = lane; i < hidden; i += 64)
+    yr[i] = T::from_float(T::lo(xr[i]) * (inv * T::lo(w[i])));
+}
+
+template <class T>
+static int rmsnorm_launch(const void *input, const void *weight, void *output,
+                          int64_t rows, int64_t hidden, int64_t in_stride,
+                          int64_t out_stride, float eps, hipStream_t st) {
+  const uint16_t *x = (const uint16_t *)input;
+  const uint16_t *w = (const uint16_t *)weight;
+  uint16_t *y = (uint16_t *)output;
+  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+  const bool vec = hidden % 8 == 0 && in_stride % 8 == 0 &&
+                   out_stride % 8 == 0 && aligned16(x) && aligned16(w) &&
+                   aligned16(y);
+  const int nvec = (int)(hidden / 8);
+  int h = (int)hidden;
+  if (vec && nvec <= 64)
+    rmsnorm_vec_kernel<T, 1><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+  else if (vec && nvec <= 128)
+    rmsnorm_vec_kernel<T, 2><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+  else if (vec && nvec <= 256)
+    rmsnorm_vec_kernel<T, 4><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+  else if (vec && nvec <= 384)
+    rmsnorm_vec_kernel<T, 6><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+  else if (vec && nvec <= 512)
+    rmsnorm_vec_kernel<T, 8><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+  else if (vec && nvec <= 1024)
+    rmsnorm_vec_kernel<T, 16><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+  else
+    rmsnorm_generic_kernel<T><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+  return check_launch("mce_rmsnorm");
+}
+
+// =========================================================================
+// SwiGLU  (reference: csrc/kernels/swiglu.cu:8-27)
+// out[t, j] = silu(g) * u, g = gate_up[t, j], u = gate_up[t, I + j].
+// Grid-stride over 8-element groups of the output; every row is computed.
+// =========================================================================
+template <class T>
+__device__ inline float silu_mul(float g, float u) {
+  return g / (1.0f + __expf(-g)) * u;
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void swiglu_vec_kernel(
+    const uint16_t *__restrict__ gu, uint16_t *__restrict__ out, int64_t rows,
+    int64_t inter, int64_t in_stride, int64_t out_stride) {
+  const int64_t groups_per_row = inter >> 3;
+  const int64_t total = rows * groups_per_row;
+  for (int64_t gi = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; gi < total;
+       gi += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = gi / groups_per_row;
+    const int64_t c = (gi - r * groups_per_row) << 3;
+    const uint16_t *src = gu + r * in_stride + c;
+    u32x4 g = *reinterpret_cast<const u32x4 *>(src);
+    u32x4 u = *reinterpret_cast<const u32x4 *>(src + inter);
+    u32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      o[k] = pack2<T>(silu_mul<T>(T::lo(g[k]), T::lo(u[k])),
+                      silu_mul<T>(T::hi(g[k]), T::hi(u[k])));
+    *reinterpret_cast<u32x4 *>(out + r * out_stride + c) = o;
+  }
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void swiglu_generic_kernel(
+    const uint16_t *__restrict__ gu, uint16_t *__restrict__ out, int64_t rows,
+    int64_t inter, int64_t in_stride, int64_t out_stride) {
+  const int64_t total = rows * inter;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / inter, c = i - r * inter;
+    const uint16_t *src = gu + r * in_stride + c;
+    out[r * out_stride + c] =
+        T::from_float(silu_mul<T>(T::lo(src[0]), T::lo(src[inter])));
+  }
+}
+
+template <class T>
+static int swiglu_launch(const void *gate_up, void *output, int64_t rows,
+                         int64_t inter, int64_t in_stride, int64_t out_stride,
+                         hipStream_t st) {
+  const uint16_t *gu = (const uint16_t *)gate_up;
+  uint16_t *out = (uint16_t *)output;
+  const bool vec = inter % 8 == 0 && in_stride % 8 == 0 &&
+                   out_stride % 8 == 0 && aligned16(gu) && aligned16(out);
+  const int64_t work = vec ? rows * (inter / 8) : rows * inter;
+  int64_t blocks = (work + 255) / 256;
+  if (blocks > 256 * 64) blocks = 256 * 64;  // grid-stride beyond this
+  if (blocks < 1) blocks = 1;
+  if (vec)
+    swiglu_vec_kernel<T><<<(unsigned)blocks, 256, 0, st>>>(gu, out, rows, inter, in_stride, out_stride);
+  else
+    swiglu_generic_kernel<T><<<(unsigned)blocks, 256, 0, st>>>(gu, out, rows, inter, in_stride, out_stride);
+  return check_launch("mce_swiglu");
+}
+
+// =========================================================================
+// Paged KV store  (reference: csrc/kernels/paged_kv.cu:7-43)
+// One lane per 16-byte piece of one (token, head) row; K and V both.
+// Bit-exact copy.  Slots < 0 or beyond the pool are skipped.
+// =========================================================================
+__global__ __launch_bounds__(256) void kv_store_vec_kernel(
+    const uint16_t *__restrict__ key, const uint16_t *__restrict__ value,
+    uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+    const int32_t *__restrict__ slots, int64_t num_tokens, int heads,
+    int head_dim, int block_size, int64_t num_slots, int64_t ks_tok,
+    int64_t ks_head, int64_t vs_tok, int64_t vs_head) {
+  const int pieces = head_dim >> 3;
+  const int64_t per_tok = (int64_t)heads * pieces;
+  const int64_t total = num_tokens * per_tok;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = i / per_tok;
+    const int rem = (int)(i - n * per_tok);
+    const int h = rem / pieces, p = rem - h * pieces;
+    const int64_t s = slots[n];
+    if (s < 0 || s >= num_slots) continue;
+    // [block, offset, head] rows are contiguous in slot order.
+    const int64_t dst = (s * heads + h) * head_dim + p * 8;
+    *reinterpret_cast<u32x4 *>(kc + dst) =
+        *reinterpret_cast<const u32x4 *>(key + n * ks_tok + h * ks_head + p * 8);
+    *reinterpret_cast<u32x4 *>(vc + dst) =
+        *reinterpret_cast<const u32x4 *>(value + n * vs_tok + h * vs_head + p * 8);
+  }
+}
+
+__global__ __launch_bounds__(256) void kv_store_generic_kernel(
+    const uint16_t *__restrict__ key, const uint16_t *__restrict__ value,
+    uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+    const int32_t *__restrict__ slots, int64_t num_tokens, int heads,
+    int head_dim, int block_size, int64_t num_slots, int64_t ks_tok,
+    int64_t ks_head, int64_t vs_tok, int64_t vs_head) {
+  const int64_t per_tok = (int64_t)heads * head_dim;
+  const int64_t total = num_tokens * per_tok;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t n = i / per_tok;
+    const int rem = (int)(i - n * per_tok);
+    const int h = rem / head_dim, d = rem - h * head_dim;
+    const int64_t s = slots[n];
+    if (s < 0 || s >= num_slots) continue;
+    const int64_t dst = (s * heads + h) * head_dim + d;
+    kc[dst] = key[n * ks_tok + h * ks_head + d];
+    vc[dst] = value[n * vs_tok + h * vs_head + d];
+  }
+}
+
+// =========================================================================
+// In-place RoPE  (reference: csrc/kernels/rope.cu:6-62; tables
+// engine/models/llama.py:47-57)
+// One lane per 4 rotation pairs of one (token, head): 8-byte loads of
+// x[i..i+3] and x[i+D/2..], 16-byte loads of cos/sin.  Q heads and K heads
+// share the launch (heads >= num_heads index K).
+// =========================================================================
+template <class T>
+__device__ inline void rope_rotate4(uint16_t *p, int half, const float *c4,
+                                    const float *s4) {
+  u32x2 a = *reinterpret_cast<const u32x2 *>(p);
+  u32x2 b = *reinterpret_cast<const u32x2 *>(p + half);
+  float x0[4] = {T::lo(a[0]), T::hi(a[0]), T::lo(a[1]), T::hi(a[1])};
+  float x1[4] = {T::lo(b[0]), T::hi(b[0]), T::lo(b[1]), T::hi(b[1])};
+  float r0[4], r1[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    r0[k] = x0[k] * c4[k] - x1[k] * s4[k];
+    r1[k] = x0[k] * s4[k] + x1[k] * c4[k];
+  }
+  u32x2 oa, ob;
+  oa[0] = pack2<T>(r0[0], r0[1]);
+  oa[1] = pack2<T>(r0[2], r0[3]);
+  ob[0] = pack2<T>(r1[0], r1[1]);
+  ob[1] = pack2<T>(r1[2], r1[3]);
+  *reinterpret_cast<u32x2 *>(p) = oa;
+  *reinterpret_cast<u32x2 *>(p + half) = ob;
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void rope_vec_kernel(
+    uint16_t *__restrict__ q, uint16_t *__restrict__ k,
+    const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+    const int32_t *__restrict__ pos, int64_t tokens, int seq_len,
+    int num_heads, int num_kv_heads, int head_dim, int64_t table_rows,
+    int64_t qsb, int64_t qss, int64_t qsh, int64_t ksb, int64_t kss,
+    int64_t ksh) {
+  const int half = head_dim >> 1;
+  const int quads = half >> 2;
+  const int heads = num_heads + num_kv_heads;
+  const int64_t per_tok = (int64_t)heads * quads;
+  const int64_t total = tokens * per_tok;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / per_tok;
+    const int rem = (int)(i - t * per_tok);
+    const int h = rem / quads, qd = rem - h * quads;
+    const int64_t ps = pos[t];
+    if (ps < 0 || ps >= table_rows) continue;
+    const int64_t b = t / seq_len, s = t - b * seq_len;
+    uint16_t *p = h < num_heads
+                      ? q + b * qsb + s * qss + h * qsh
+                      : k + b * ksb + s * kss + (h - num_heads) * ksh;
+    floatx4 c = *reinterpret_cast<const floatx4 *>(cos_t + ps * half + qd * 4);
+    floatx4 sn = *reinterpret_cast<const floatx4 *>(sin_t + ps * half + qd * 4);
+    float c4[4] = {c[0], c[1], c[2], c[3]};
+    float s4[4] = {sn[0], sn[1], sn[2], sn[3]};
+    rope_rotate4<T>(p + qd * 4, half, c4, s4);
+  }
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void rope_generic_kernel(
+    uint16_t *__restrict__ q, uint16_t *__restrict__ k,
+    const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+    const int32_t *__restrict__ pos, int64_t tokens, int seq_len,
+    int num_heads, int num_kv_heads, int head_dim, int64_t table_rows,
+    int64_t qsb, int64_t qss, int64_t qsh, int64_t ksb, int64_t kss,
+    int64_t ksh) {
+  const int half = head_dim >> 1;
+  const int heads = num_heads + num_kv_heads;
+  const int64_t per_tok = (int64_t)heads * half;
+  const int64_t total = tokens * per_tok;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / per_tok;
+    const int rem = (int)(i - t * per_tok);
+    const int h = rem / half, d = rem - h * half;
+    const int64_t ps = pos[t];
+    if (ps < 0 || ps >= table_rows) continue;
+    const int64_t b = t / seq_len, s = t - b * seq_len;
+    uint16_t *p = h < num_heads
+                      ? q + b * qsb + s * qss + h * qsh
+                      : k + b * ksb + s * kss + (h - num_heads) * ksh;
+    const float c = cos_t[ps * half + d], sn = sin_t[ps * half + d];
+    const float x0 = T::lo(p[d]), x1 = T::lo(p[d + half]);
+    p[d] = T::from_float(x0 * c - x1 * sn);
+    p[d + half] = T::from_float(x0 * sn + x1 * c);
+  }
+}
+
+static unsigned grid_for(int64_t work) {
+  int64_t blocks = (work + 255) / 256;
+  if (blocks > 256 * 64) blocks = 256 * 64;
+  return (unsigned)(blocks < 1 ? 1 : blocks);
+}
+
+}  // namespace mce
+
+using namespace mce;
+
+extern "C" int mce_rmsnorm(int dtype, const void *input, const void *weight,
+                           void *output, int64_t rows, int64_t hidden,
+                           int64_t in_row_stride, int64_t out_row_stride,
+                           float eps, void *stream) {
+  clear_error();
+  MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16, "mce_rmsnorm: unknown dtype %d", dtype);
+  MCE_REQUIRE(rows >= 0 && hidden >= 1 && hidden <= (1 << 24),
+              "mce_rmsnorm: bad shape rows=%lld hidden=%lld", (long long)rows, (long long)hidden);
+  MCE_REQUIRE(in_row_stride >= hidden && out_row_stride >= hidden,
+              "mce_rmsnorm: row stride smaller than hidden size");
+  if (rows == 0) return MCE_OK;
+  MCE_REQUIRE(input && weight && output, "mce_rmsnorm: null pointer");
+  MCE_REQUIRE((rows + 3) / 4 < (int64_t)1 << 31, "mce_rmsnorm: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  return dtype == MCE_F16
+             ? rmsnorm_launch<F16T>(input, weight, output, rows, hidden, in_row_stride, out_row_stride, eps, st)
+             : rmsnorm_launch<BF16T>(input, weight, output, rows, hidden, in_row_stride, out_row_stride, eps, st);
+}
+
+extern "C" int mce_swiglu(int dtype, const void *gate_up, void *output,
+                          int64_t rows, int64_t inter, int64_t in_row_stride,
+                          int64_t out_row_stride, void *stream) {
+  clear_error();
+  MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16, "mce_swiglu: unknown dtype %d", dtype);
+  MCE_REQUIRE(rows >= 0 && inter >= 0, "mce_swiglu: bad shape");
+  MCE_REQUIRE(in_row_stride >= 2 * inter && out_row_stride >= inter,
+              "mce_swiglu: row stride smaller than row");
+  if (rows == 0 || inter == 0) return MCE_OK;
+  MCE_REQUIRE(gate_up && output, "mce_swiglu: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  return dtype == MCE_F16
+             ? swiglu_launch<F16T>(gate_up, output, rows, inter, in_row_stride, out_row_stride, st)
+             : swiglu_launch<BF16T>(gate_up, output, rows, inter, in_row_stride, out_row_stride, st);
+}
+
+extern "C" int mce_paged_kv_store(int dtype, const void *key, const void *value,
+                                  void *key_cache, void *value_cache,
+                                  const int32_t *slot_mapping,
+                                  int64_t num_tokens, int num_kv_heads,
+                                  int head_dim, int block_size,
+                                  int64_t num_blocks, int64_t key_stride_tok,
+                                  int64_t key_stride_head,
+                                  int64_t value_stride_tok,
+                                  int64_t value_stride_head, void *stream) {
+  clear_error();
+  MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16, "mce_paged_kv_store: unknown dtype %d", dtype);
+  MCE_REQUIRE(num_tokens >= 0 && num_kv_heads >= 1 && head_dim >= 1 &&
+                  block_size >= 1 && num_blocks >= 0,
+              "mce_paged_kv_store: bad shape");
+  if (num_tokens == 0 || num_blocks == 0) return MCE_OK;
+  MCE_REQUIRE(key && value && key_cache && value_cache && slot_mapping,
+              "mce_paged_kv_store: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t num_slots = num_blocks * block_size;
+  const bool vec = head_dim % 8 == 0 && key_stride_tok % 8 == 0 &&
+                   key_stride_head % 8 == 0 && value_stride_tok % 8 == 0 &&
+                   value_stride_head % 8 == 0 && aligned16(key) &&
+                   aligned16(value) && aligned16(key_cache) &&
+                   aligned16(value_cache);
+  const int64_t work = num_tokens * num_kv_heads * (vec ? head_dim / 8 : head_dim);
+  if (vec)
+    kv_store_vec_kernel<<<grid_for(work), 256, 0, st>>>(
+        (const uint16_t *)key, (const uint16_t *)value, (uint16_t *)key_cache,
+        (uint16_t *)value_cache, slot_mapping, num_tokens, num_kv_heads,
+        head_dim, block_size, num_slots, key_stride_tok, key_stride_head,
+        value_stride_tok, value_stride_head);
+  else
+    kv_store_generic_kernel<<<grid_for(work), 256, 0, st>>>(
+        (const uint16_t *)key, (const uint16_t *)value, (uint16_t *)key_cache,
+        (uint16_t *)value_cache, slot_mapping, num_tokens, num_kv_heads,
+        head_dim, block_size, num_slots, key_stride_tok, key_stride_head,
+        value_stride_tok, value_stride_head);
+  return check_launch("mce_paged_kv_store");
+}
+
+extern "C" int mce_rope_inplace(int dtype, void *query, void *key,
+                                const float *cos_table, const float *sin_table,
+                                const int32_t *positions, int batch,
+                                int seq_len, int num_heads, int num_kv_heads,
+                                int head_dim, int64_t table_rows,
+                                int64_t q_stride_b, int64_t q_stride_s,
+                                int64_t q_stride_h, int64_t k_stride_b,
+                                int64_t k_stride_s, int64_t k_stride_h,
+                                void *stream) {
+  clear_error();
+  MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16, "mce_rope_inplace: unknown dtype %d", dtype);
+  MCE_REQUIRE(batch >= 0 && seq_len >= 0 && num_heads >= 0 && head_dim >= 2 &&
+                  head_dim % 2 == 0 && table_rows >= 0,
+              "mce_rope_inplace: bad shape");
+  if (!key) num_kv_heads = 0;
+  MCE_REQUIRE(num_kv_heads >= 0, "mce_rope_inplace: bad num_kv_heads");
+  const int64_t tokens = (int64_t)batch * seq_len;
+  if (tokens == 0 || num_heads + num_kv_heads == 0) return MCE_OK;
+  MCE_REQUIRE(query && cos_table && sin_table && positions,
+              "mce_rope_inplace: null pointer");
+  hipStream_t st = (hipStream_t)stream;
+  const int half = head_dim / 2;
+  bool vec = half % 4 == 0 && q_stride_b % 4 == 0 && q_stride_s % 4 == 0 &&
+             q_stride_h % 4 == 0 && (reinterpret_cast<uintptr_t>(query) & 7) == 0 &&
+             aligned16(cos_table) && aligned16(sin_table);
+  if (key)
+    vec = vec && k_stride_b % 4 == 0 && k_stride_s % 4 == 0 &&
+          k_stride_h % 4 == 0 && (reinterpret_cast<uintptr_t>(key) & 7) == 0;
+  const int heads = num_heads + num_kv_heads;
+  uint16_t *q = (uint16_t *)query, *k = (uint16_t *)key;
+  if (vec) {
+    const int64_t work = tokens * heads * (half / 4);
+    if (dtype == MCE_F16)
+      rope_vec_kernel<F16T><<<grid_for(work), 256, 0, st>>>(q, k, cos_table, sin_table, positions, tokens, seq_len, num_heads, num_kv_heads, head_dim, table_rows, q_stride_b, q_stride_s, q_stride_h, k_stride_b, k_stride_s, k_stride_h);
+    else
+      rope_vec_kernel<BF16T><<<grid_for(work), 256, 0, st>>>(q, k, cos_table, sin_table, positions, tokens, seq_len, num_heads, num_kv_heads, head_dim, table_rows, q_stride_b, q_stride_s, q_stride_h, k_stride_b, k_stride_s, k_stride_h);
+  } else {
+    const int64_t work = tokens * heads * half;
+    if (dtype == MCE_F16)
+      rope_generic_kernel<F16T><<<grid_for(work), 256, 0, st>>>(q, k, cos_table, sin_table, positions, tokens, seq_len, num_heads, num_kv_heads, head_dim, table_rows, q_stride_b, q_stride_s, q_stride_h, k_stride_b, k_stride_s, k_stride_h);
+    else
+      rope_generic_kernel<BF16T><<<grid_for(work), 256, 0, st>>>(q, k, cos_table, sin_table, positions, tokens, seq_len, num_heads, num_kv_heads, head_dim, table_rows, q_stride_b, q_stride_s, q_stride_h, k_stride_b, k_stride_s, k_stride_h);
+  }
+  return check_launch("mce_rope_inplace");
+}

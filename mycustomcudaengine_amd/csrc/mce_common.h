@@ -1,0 +1,131 @@
+// Shared host/device helpers for the gfx950 kernels of libmce.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/mce_abi.h"
+
+namespace mce {
+
+// ---------------------------------------------------------------- host side
+
+// Records a formatted message for mce_last_error() and returns `code`.
+int set_error(int code, const char *fmt, ...);
+void clear_error();
+
+// Maps a failed launch (hipGetLastError after the launch) to MCE_ERR_LAUNCH.
+int check_launch(const char *what);
+
+inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
+inline int ilog2(int64_t x) {
+  int r = 0;
+  while ((int64_t(1) << r) < x) ++r;
+  return r;
+}
+inline bool aligned16(const void *p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+#define MCE_REQUIRE(cond, ...)                                                 \
+  do {                                                                         \
+    if (!(cond)) return ::mce::set_error(MCE_ERR_INVALID, __VA_ARGS__);        \
+  } while (0)
+
+// -------------------------------------------------------------- device side
+
+typedef _Float16 f16;
+typedef uint16_t bf16_bits;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Storage-type traits: conversion of 16-bit storage values to/from fp32.
+struct F16T {
+  static constexpr int code = MCE_F16;
+  __device__ static inline float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(f16, (uint16_t)(w & 0xffffu));
+  }
+  __device__ static inline float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(f16, (uint16_t)(w >> 16));
+  }
+  __device__ static inline uint16_t from_float(float x) {
+    return __builtin_bit_cast(uint16_t, (f16)x);
+  }
+};
+
+struct BF16T {
+  static constexpr int code = MCE_BF16;
+  __device__ static inline float lo(uint32_t w) {
+    return __builtin_bit_cast(float, w << 16);
+  }
+  __device__ static inline float hi(uint32_t w) {
+    return __builtin_bit_cast(float, w & 0xffff0000u);
+  }
+  // Round to nearest even; NaN stays NaN.
+  __device__ static inline uint16_t from_float(float x) {
+    uint32_t u = __builtin_bit_cast(uint32_t, x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+  }
+};
+
+template <class T>
+__device__ inline uint32_t pack2(float a, float b) {
+  return (uint32_t)T::from_float(a) | ((uint32_t)T::from_float(b) << 16);
+}
+
+// 16-lane row reductions with DPP (every lane of the row gets the result).
+// quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E, row_ror:4 = 0x124,
+// row_ror:8 = 0x128.
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                         0xf, 0xf, false));
+}
+
+__device__ inline float row16_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x124>(v));
+  v = fmaxf(v, dpp_f<0x128>(v));
+  return v;
+}
+
+__device__ inline float row16_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x124>(v);
+  v += dpp_f<0x128>(v);
+  return v;
+}
+
+// Full 64-lane sum; every lane gets the result.
+__device__ inline float wave_sum(float v) {
+  v = row16_sum(v);
+  v += __shfl_xor(v, 16, 64);
+  v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+__device__ inline float wave_max(float v) {
+  v = row16_max(v);
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  v = fmaxf(v, __shfl_xor(v, 32, 64));
+  return v;
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace mce

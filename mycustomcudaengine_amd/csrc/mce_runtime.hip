@@ -1,0 +1,30 @@
+// Error reporting and version entry points of libmce.so.
+#include "mce_common.h"
+
+namespace mce {
+
+static thread_local char g_last_error[512] = {0};
+
+int set_error(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+void clear_error() { g_last_error[0] = 0; }
+
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess)
+    return set_error(MCE_ERR_LAUNCH, "%s: launch failed: %s", what,
+                     hipGetErrorString(e));
+  return MCE_OK;
+}
+
+}  // namespace mce
+
+extern "C" const char *mce_last_error(void) { return mce::g_last_error; }
+
+extern "C" int mce_abi_version(void) { return 100; }

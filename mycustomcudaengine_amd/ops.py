@@ -1,0 +1,261 @@
+"""The `my_cuda_engine_cpp` op surface on PyTorch-ROCm tensors.
+
+Same six names, positional arguments and return conventions as the
+reference's pybind module (csrc/bindings.cpp:4-19,22-29):
+
+    rmsnorm(input, weight, eps) -> Tensor
+    swiglu(gate_up) -> Tensor
+    paged_kv_store(key, value, key_cache, value_cache, slot_mapping) -> None
+    paged_attention_decode(query, key_cache, value_cache, block_tables,
+                           context_lens, max_blocks_per_seq, block_size,
+                           scale) -> Tensor
+    rope_inplace(query, key, cos_table, sin_table, positions) -> None
+    prefill_attention(query, key, value, scale) -> Tensor
+
+Each op validates dtype, device, shape and layout on the host and raises
+RuntimeError (the exception type TORCH_CHECK raises in the reference), then
+calls libmce.so on torch's current HIP stream.  Outputs and the decode
+workspace are allocated with torch, so every op can be recorded by
+torch.cuda.graph (hipGraph).  No op synchronises or reads device memory on the
+host.  There is no CPU path: CPU tensors are rejected.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "rmsnorm",
+    "swiglu",
+    "paged_kv_store",
+    "paged_attention_decode",
+    "rope_inplace",
+    "prefill_attention",
+]
+
+_DTYPES = {torch.float16: _lib.MCE_F16, torch.bfloat16: _lib.MCE_BF16}
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _dtype_code(t: torch.Tensor, name: str) -> int:
+    code = _DTYPES.get(t.dtype)
+    _check(code is not None, f"{name} must be float16 or bfloat16 (got {t.dtype})")
+    return code
+
+
+def _on_gpu(name: str, *ts: torch.Tensor) -> torch.device:
+    dev = ts[0].device
+    for t in ts:
+        _check(isinstance(t, torch.Tensor), f"{name}: expected tensors")
+        _check(t.is_cuda, f"{name}: tensors must be on a GPU (got {t.device})")
+        _check(t.device == dev, f"{name}: tensors are on different devices")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+class _on_device:
+    """Makes `dev` current for the duration of a call (a device guard)."""
+
+    def __init__(self, dev: torch.device):
+        self.dev = dev
+        self.prev = None
+
+    def __enter__(self):
+        cur = torch.cuda.current_device()
+        if cur != self.dev.index:
+            self.prev = cur
+            torch.cuda.set_device(self.dev)
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+
+
+def rmsnorm(input: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """Fused RMSNorm over the last dim (reference: csrc/kernels/rmsnorm.cu:110-130)."""
+    dev = _on_gpu("rmsnorm", input, weight)
+    code = _dtype_code(input, "rmsnorm input")
+    _check(weight.dtype == input.dtype, "rmsnorm: weight dtype must match input")
+    _check(input.dim() >= 1, "rmsnorm: input must have at least one dim")
+    hidden = input.size(-1)
+    _check(weight.dim() == 1 and weight.size(0) == hidden and weight.is_contiguous(),
+           f"rmsnorm: weight must be contiguous [{hidden}]")
+    x = input if input.is_contiguous() else input.contiguous()
+    out = torch.empty_like(x)
+    rows = x.numel() // hidden if hidden else 0
+    with _on_device(dev):
+        _lib.call("mce_rmsnorm", code, x.data_ptr(), weight.data_ptr(), out.data_ptr(),
+                  rows, hidden, hidden, hidden, float(eps), _stream(dev))
+    return out
+
+
+def swiglu(gate_up: torch.Tensor) -> torch.Tensor:
+    """silu(first half) * second half of the last dim (reference: swiglu.cu:29-52)."""
+    dev = _on_gpu("swiglu", gate_up)
+    code = _dtype_code(gate_up, "swiglu gate_up")
+    _check(gate_up.dim() >= 1, "swiglu: input must have at least one dim")
+    two_i = gate_up.size(-1)
+    _check(two_i % 2 == 0, f"swiglu: last dim must be even (got {two_i})")
+    x = gate_up if gate_up.is_contiguous() else gate_up.contiguous()
+    inter = two_i // 2
+    shape = list(x.shape)
+    shape[-1] = inter
+    out = torch.empty(shape, dtype=x.dtype, device=x.device)
+    rows = x.numel() // two_i if two_i else 0
+    with _on_device(dev):
+        _lib.call("mce_swiglu", code, x.data_ptr(), out.data_ptr(), rows, inter, two_i,
+                  inter, _stream(dev))
+    return out
+
+
+def paged_kv_store(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
+                   value_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Scatter per-token K/V rows into the paged pools (reference: paged_kv.cu:45-69).
+
+    key/value: [N, Hkv, D] (any token/head strides, contiguous last dim);
+    caches: contiguous [num_blocks, block_size, Hkv, D]; slot_mapping int32 [N].
+    """
+    dev = _on_gpu("paged_kv_store", key, value, key_cache, value_cache, slot_mapping)
+    code = _dtype_code(key, "paged_kv_store key")
+    for t, n in ((value, "value"), (key_cache, "key_cache"), (value_cache, "value_cache")):
+        _check(t.dtype == key.dtype, f"paged_kv_store: {n} dtype must match key")
+    _check(key.dim() == 3 and value.shape == key.shape,
+           f"paged_kv_store: key/value must be [N, Hkv, D] (got {tuple(key.shape)}, "
+           f"{tuple(value.shape)})")
+    n_tok, hkv, d = key.shape
+    _check(key_cache.dim() == 4 and key_cache.shape == value_cache.shape,
+           "paged_kv_store: caches must be [num_blocks, block_size, Hkv, D]")
+    nb, bs, chkv, cd = key_cache.shape
+    _check(chkv == hkv and cd == d,
+           f"paged_kv_store: cache head shape {(chkv, cd)} != key head shape {(hkv, d)}")
+    _check(key_cache.is_contiguous() and value_cache.is_contiguous(),
+           "paged_kv_store: caches must be contiguous")
+    _check(key.stride(-1) == 1 and value.stride(-1) == 1,
+           "paged_kv_store: key/value last dim must be contiguous")
+    _check(slot_mapping.dtype == torch.int32 and slot_mapping.dim() == 1 and
+           slot_mapping.size(0) == n_tok and slot_mapping.is_contiguous(),
+           f"paged_kv_store: slot_mapping must be contiguous int32 [{n_tok}]")
+    with _on_device(dev):
+        _lib.call("mce_paged_kv_store", code, key.data_ptr(), value.data_ptr(),
+                  key_cache.data_ptr(), value_cache.data_ptr(), slot_mapping.data_ptr(),
+                  n_tok, hkv, d, bs, nb, key.stride(0), key.stride(1),
+                  value.stride(0), value.stride(1), _stream(dev))
+
+
+def paged_attention_decode(query: torch.Tensor, key_cache: torch.Tensor,
+                           value_cache: torch.Tensor, block_tables: torch.Tensor,
+                           context_lens: torch.Tensor, max_blocks_per_seq: int,
+                           block_size: int, scale: float) -> torch.Tensor:
+    """One-token paged attention with GQA (reference: flash_attn_paged.cu:144-168).
+
+    query [B, Hq, D]; caches [num_blocks, block_size, Hkv, D];
+    block_tables int32 [B, max_blocks_per_seq]; context_lens int32 [B].
+    Returns a new [B, Hq, D] tensor.  Rows with context_len 0 are zeros.
+    """
+    dev = _on_gpu("paged_attention_decode", query, key_cache, value_cache,
+                  block_tables, context_lens)
+    code = _dtype_code(query, "paged_attention_decode query")
+    _check(key_cache.dtype == query.dtype and value_cache.dtype == query.dtype,
+           "paged_attention_decode: cache dtype must match query")
+    _check(query.dim() == 3, "paged_attention_decode: query must be [B, Hq, D]")
+    b, hq, d = query.shape
+    _check(key_cache.dim() == 4 and key_cache.shape == value_cache.shape,
+           "paged_attention_decode: caches must be [num_blocks, block_size, Hkv, D]")
+    nb, bs, hkv, cd = key_cache.shape
+    _check(cd == d, f"paged_attention_decode: cache head_dim {cd} != query head_dim {d}")
+    _check(int(block_size) == bs,
+           f"paged_attention_decode: block_size {block_size} != cache block size {bs}")
+    _check(key_cache.is_contiguous() and value_cache.is_contiguous(),
+           "paged_attention_decode: caches must be contiguous")
+    mb = int(max_blocks_per_seq)
+    _check(block_tables.dtype == torch.int32 and block_tables.dim() == 2 and
+           block_tables.size(0) == b and block_tables.size(1) == mb and
+           block_tables.is_contiguous(),
+           f"paged_attention_decode: block_tables must be contiguous int32 [{b}, {mb}] "
+           f"(got {block_tables.dtype} {tuple(block_tables.shape)})")
+    _check(context_lens.dtype == torch.int32 and context_lens.dim() == 1 and
+           context_lens.size(0) == b and context_lens.is_contiguous(),
+           f"paged_attention_decode: context_lens must be contiguous int32 [{b}]")
+    q = query if query.is_contiguous() else query.contiguous()
+    out = torch.empty_like(q)
+    with _on_device(dev):
+        lib = _lib.load()
+        ws_bytes = lib.mce_paged_attention_decode_workspace_size(b, hq, mb, bs) if b else 0
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
+        _lib.call("mce_paged_attention_decode", code, q.data_ptr(), key_cache.data_ptr(),
+                  value_cache.data_ptr(), block_tables.data_ptr(), context_lens.data_ptr(),
+                  out.data_ptr(), b, hq, hkv, d, mb, bs, nb, float(scale),
+                  ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev))
+    return out
+
+
+def rope_inplace(query: torch.Tensor, key, cos_table: torch.Tensor,
+                 sin_table: torch.Tensor, positions: torch.Tensor) -> None:
+    """Rotate Q (and K) in place, half-split form (reference: rope.cu:64-99).
+
+    query [B, S, Hq, D], key [B, S, Hkv, D] or None (any strides with a
+    contiguous last dim); cos/sin fp32 [P, D/2]; positions int32 [B, S].
+    """
+    tensors = [query, cos_table, sin_table, positions] + ([key] if key is not None else [])
+    dev = _on_gpu("rope_inplace", *tensors)
+    code = _dtype_code(query, "rope_inplace query")
+    _check(query.dim() == 4, "rope_inplace: query must be [B, S, Hq, D]")
+    b, s, hq, d = query.shape
+    _check(d % 2 == 0, f"rope_inplace: head_dim must be even (got {d})")
+    _check(query.stride(-1) == 1, "rope_inplace: query last dim must be contiguous")
+    hkv = 0
+    if key is not None:
+        _check(key.dtype == query.dtype, "rope_inplace: key dtype must match query")
+        _check(key.dim() == 4 and key.size(0) == b and key.size(1) == s and key.size(3) == d,
+               f"rope_inplace: key must be [{b}, {s}, Hkv, {d}] (got {tuple(key.shape)})")
+        _check(key.stride(-1) == 1, "rope_inplace: key last dim must be contiguous")
+        hkv = key.size(2)
+    for t, n in ((cos_table, "cos_table"), (sin_table, "sin_table")):
+        _check(t.dtype == torch.float32 and t.dim() == 2 and t.size(1) == d // 2 and
+               t.is_contiguous(), f"rope_inplace: {n} must be contiguous fp32 [P, {d // 2}]")
+    _check(cos_table.size(0) == sin_table.size(0), "rope_inplace: table lengths differ")
+    _check(positions.dtype == torch.int32 and positions.numel() == b * s and
+           positions.is_contiguous(),
+           f"rope_inplace: positions must be contiguous int32 with {b * s} elements")
+    ks = key.stride() if key is not None else (0, 0, 0, 0)
+    with _on_device(dev):
+        _lib.call("mce_rope_inplace", code, query.data_ptr(),
+                  key.data_ptr() if key is not None else None, cos_table.data_ptr(),
+                  sin_table.data_ptr(), positions.data_ptr(), b, s, hq, hkv, d,
+                  cos_table.size(0), query.stride(0), query.stride(1), query.stride(2),
+                  ks[0], ks[1], ks[2], _stream(dev))
+
+
+def prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                      scale: float) -> torch.Tensor:
+    """Causal GQA attention on contiguous Q/K/V (reference: prefill_attention.cu:271-309).
+
+    query [B, S, Hq, D]; key/value [B, S, Hkv, D].  Returns [B, S, Hq, D].
+    """
+    dev = _on_gpu("prefill_attention", query, key, value)
+    code = _dtype_code(query, "prefill_attention query")
+    _check(key.dtype == query.dtype and value.dtype == query.dtype,
+           "prefill_attention: key/value dtype must match query")
+    _check(query.dim() == 4 and key.dim() == 4 and value.shape == key.shape,
+           "prefill_attention: expected query [B, S, Hq, D], key/value [B, S, Hkv, D]")
+    b, s, hq, d = query.shape
+    _check(key.size(0) == b and key.size(1) == s and key.size(3) == d,
+           f"prefill_attention: key shape {tuple(key.shape)} does not match query "
+           f"{tuple(query.shape)}")
+    hkv = key.size(2)
+    q = query if query.is_contiguous() else query.contiguous()
+    k = key if key.is_contiguous() else key.contiguous()
+    v = value if value.is_contiguous() else value.contiguous()
+    out = torch.empty_like(q)
+    with _on_device(dev):
+        _lib.call("mce_prefill_attention", code, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                  out.data_ptr(), b, s, hq, hkv, d, float(scale), _stream(dev))
+    return out

@@ -1,0 +1,29 @@
+"""CPU oracle of the attention hot path -- TEST INFRASTRUCTURE ONLY.
+
+This package restates, on the CPU, the semantics of the reference's hot-path
+ops (paths relative to the reference checkout; each function cites the lines
+it follows).  Floating-point ops run in torch fp32 (or fp64) on the CPU;
+integer/index work (slot mapping, block allocation, the KV scatter) runs in
+numpy or plain Python.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import it, and only as the checker or the timed CPU baseline -- never as the
+product path.  The product ops (mycustomcudaengine_amd.ops) have no CPU
+fallback.
+
+How each function is pinned (tests/test_oracle.py):
+  decode_attention_ref   torch SDPA (enable_gqa) on the gathered KV, a scalar
+                         brute force on tiny inputs, block-table permutation
+                         invariance, NaN-sentinel pool, ctx == 1 -> v_0.
+  prefill_attention_ref  causal torch SDPA (enable_gqa), scalar brute force,
+                         S == 1 -> v_0, row 0 -> v_0.
+  rmsnorm_ref            torch.nn.functional.rms_norm, scalar brute force.
+  rope_tables/rope_ref   complex-exponential rotation, pos 0 == identity,
+                         per-pair norm preservation, composition of angles.
+  swiglu_ref             torch.nn.functional.silu, math.exp brute force.
+  kv_store_ref           scalar Python loop; slot < 0 skipped.
+  BlockAllocatorRef      hand-enumerated FIFO sequences.
+  slot_mapping_ref       brute force over the allocator's tables.
+  llama_*_ref            composition of the above with fp32 GEMMs; checked
+                         against a torch-only decomposition of one layer.
+"""

@@ -1,0 +1,145 @@
+"""GPU parity of paged decode attention against the CPU oracle.
+
+Bar: max |gpu - fp32 oracle| <= 1e-2 (the reference's tolerance class,
+tests/test_paged_attention.py:86, tightened to max-abs per BASELINE), no NaN,
+block-table handling exact (NaN-filled unused pool blocks must not leak).
+"""
+import math
+
+import pytest
+import torch
+
+import my_cuda_engine_cpp as ops
+from oracle.inputs import cfg1_decode, cfg2_decode, cfg4_decode, make_decode_case
+from oracle.ops_ref import decode_attention_ref
+
+TOL = 1e-2
+pytestmark = pytest.mark.gpu
+
+
+def run_gpu(case, dev):
+    out = ops.paged_attention_decode(
+        case.query.to(dev), case.key_cache.to(dev), case.value_cache.to(dev),
+        case.block_tables.to(dev), case.context_lens.to(dev), case.max_blocks,
+        case.block_size, case.scale)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def check(case, dev, tol=TOL):
+    out = run_gpu(case, dev)
+    ref = decode_attention_ref(case.query, case.key_cache, case.value_cache,
+                               case.block_tables, case.context_lens, case.scale)
+    assert out.shape == ref.shape and out.dtype == torch.float16
+    assert not torch.isnan(out).any(), "NaN in output (pool sentinel leaked?)"
+    err = (out.float() - ref).abs().max().item()
+    assert err <= tol, f"max abs err {err}"
+    return out, ref
+
+
+def test_cfg1(dev):
+    check(cfg1_decode(), dev)
+
+
+def test_cfg2_batched_mixed_context(dev):
+    check(cfg2_decode(nan_pool=True), dev)
+
+
+def test_cfg4_long_context_split_k(dev):
+    check(cfg4_decode(), dev)
+
+
+@pytest.mark.parametrize("ctx", [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129,
+                                 255, 256, 257, 511, 513, 1000, 1024, 1025, 2049])
+def test_context_edges(dev, ctx):
+    check(make_decode_case(100 + ctx, 2, [ctx, max(1, ctx // 2 + 3)]), dev)
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 8), (16, 8), (24, 8), (32, 8), (40, 8), (64, 8),
+                                    (6, 2), (3, 1)])
+def test_gqa_groups(dev, hq, hkv):
+    check(make_decode_case(7 + hq, 3, [300, 17, 1100], num_heads=hq, num_kv_heads=hkv), dev)
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32, 64, 256])
+def test_block_sizes(dev, bs):
+    check(make_decode_case(11 + bs, 3, [700, 5, 1500], block_size=bs), dev)
+
+
+def test_ctx_one_returns_v0(dev):
+    case = make_decode_case(5, 4, [1, 1, 1, 1])
+    out = run_gpu(case, dev)
+    hkv = case.key_cache.shape[2]
+    grp = case.query.shape[1] // hkv
+    for b in range(4):
+        blk = int(case.block_tables[b, 0])
+        v0 = case.value_cache[blk, 0].repeat_interleave(grp, dim=0)
+        assert torch.equal(out[b], v0)
+
+
+def test_zero_context_rows_are_zero(dev):
+    case = make_decode_case(6, 3, [0, 40, 0])
+    out, ref = check(case, dev)
+    assert torch.count_nonzero(out[0]) == 0 and torch.count_nonzero(out[2]) == 0
+
+
+def test_block_table_permutation_invariance(dev):
+    """Physically relocating a sequence's blocks must not change its output."""
+    case = make_decode_case(8, 2, [400, 333], nan_pool=True)
+    out1 = run_gpu(case, dev)
+    kc, vc, bt = case.key_cache.clone(), case.value_cache.clone(), case.block_tables.clone()
+    nb = kc.shape[0]
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(3))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(nb)
+    kc2, vc2 = kc[perm], vc[perm]  # new block j holds old block perm[j]
+    bt2 = inv[bt.long()].to(torch.int32)
+    case.key_cache, case.value_cache, case.block_tables = kc2, vc2, bt2
+    out2 = run_gpu(case, dev)
+    assert torch.equal(out1, out2)
+
+
+def test_graph_capture_replay(dev):
+    """hipGraph capture through torch.cuda.graph; replays match eager."""
+    case = make_decode_case(9, 8, [513, 600, 17, 4000, 1, 256, 257, 3000])
+    q = case.query.to(dev)
+    kc, vc = case.key_cache.to(dev), case.value_cache.to(dev)
+    bt, cl = case.block_tables.to(dev), case.context_lens.to(dev)
+    args = (kc, vc, bt, cl, case.max_blocks, case.block_size, case.scale)
+    eager = ops.paged_attention_decode(q, *args)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.paged_attention_decode(q, *args)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static_out = ops.paged_attention_decode(q, *args)
+    for i in range(4):
+        q.copy_(case.query.to(dev) * (1.0 + 0.1 * i))
+        g.replay()
+        torch.cuda.synchronize()
+        want = ops.paged_attention_decode(q, *args)
+        torch.cuda.synchronize()
+        assert torch.equal(static_out, want), f"replay {i} differs from eager"
+    q.copy_(case.query.to(dev))
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(static_out, eager)
+
+
+def test_rejects_bad_inputs(dev):
+    case = make_decode_case(10, 1, [64])
+    q = case.query.to(dev)
+    kc, vc = case.key_cache.to(dev), case.value_cache.to(dev)
+    bt, cl = case.block_tables.to(dev), case.context_lens.to(dev)
+    with pytest.raises(RuntimeError):
+        ops.paged_attention_decode(q.float(), kc, vc, bt, cl, case.max_blocks, 16, case.scale)
+    with pytest.raises(RuntimeError):
+        ops.paged_attention_decode(q, kc, vc, bt.long(), cl, case.max_blocks, 16, case.scale)
+    with pytest.raises(RuntimeError):
+        ops.paged_attention_decode(q, kc, vc, bt, cl, case.max_blocks, 8, case.scale)
+    with pytest.raises(RuntimeError):
+        ops.paged_attention_decode(q[..., :64].contiguous(), kc[..., :64].contiguous(),
+                                   vc[..., :64].contiguous(), bt, cl, case.max_blocks, 16,
+                                   case.scale)

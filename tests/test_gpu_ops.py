@@ -1,0 +1,213 @@
+"""GPU parity of RMSNorm, SwiGLU, RoPE, the paged KV store and causal prefill
+attention against the CPU oracle.
+
+Bars: KV store bit-exact; RMSNorm/SwiGLU/RoPE/prefill max-abs <= 1e-2 vs the
+fp32 oracle (reference tolerance class: tests/test_ops.py:35,
+tests/test_rope.py:56-57); RMSNorm/SwiGLU/RoPE additionally within one fp16
+ulp-scale relative bound.
+"""
+import pytest
+import torch
+
+import my_cuda_engine_cpp as ops
+from oracle.alloc_ref import BlockAllocatorRef, prefill_slots_ref
+from oracle.inputs import cfg3_prefill, make_prefill_case
+from oracle.ops_ref import (kv_store_ref, prefill_attention_ref, rmsnorm_ref, rope_ref,
+                            rope_tables, swiglu_ref)
+
+TOL = 1e-2
+pytestmark = pytest.mark.gpu
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rel_close(out, ref, rel=2e-3, abs_=1e-3):
+    """|out - ref| <= abs_ + rel * |ref|: fp16 rounding of an exact result."""
+    d = (out.float() - ref).abs()
+    bound = abs_ + rel * ref.abs()
+    return bool((d <= bound).all()), d.max().item()
+
+
+# ------------------------------------------------------------------ RMSNorm
+@pytest.mark.parametrize("rows,hidden", [(8, 3072), (4096, 3072), (3, 4096), (5, 8192),
+                                         (7, 1000), (2, 127), (4, 8200), (1, 8), (65, 512)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_rmsnorm(dev, rows, hidden, dtype):
+    x = torch.randn(rows, hidden, generator=gen(rows * 7 + hidden)).to(dtype)
+    w = (1.0 + 0.5 * torch.randn(hidden, generator=gen(hidden))).to(dtype)
+    out = ops.rmsnorm(x.to(dev), w.to(dev), 1e-5).cpu()
+    ref = rmsnorm_ref(x, w, 1e-5)
+    ok, err = rel_close(out, ref, rel=4e-3 if dtype == torch.float16 else 1.6e-2)
+    assert ok, err
+    if dtype == torch.float16:
+        assert (out.float() - ref).abs().max().item() <= TOL
+
+
+def test_rmsnorm_3d_input(dev):
+    x = torch.randn(2, 5, 3072, generator=gen(1)).half()
+    w = torch.ones(3072).half()
+    out = ops.rmsnorm(x.to(dev), w.to(dev), 1e-5).cpu()
+    assert out.shape == x.shape
+    assert (out.float() - rmsnorm_ref(x, w, 1e-5)).abs().max() <= TOL
+
+
+# ------------------------------------------------------------------- SwiGLU
+@pytest.mark.parametrize("shape", [(8, 16384), (4096, 16384), (1, 16), (3, 14), (2, 7, 64),
+                                   (5, 1000)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_swiglu_all_rows(dev, shape, dtype):
+    x = (2.0 * torch.randn(*shape, generator=gen(sum(shape)))).to(dtype)
+    out = ops.swiglu(x.to(dev)).cpu()
+    ref = swiglu_ref(x)
+    assert out.shape == ref.shape
+    ok, err = rel_close(out, ref, rel=4e-3 if dtype == torch.float16 else 1.6e-2)
+    assert ok, err
+
+
+# --------------------------------------------------------------------- RoPE
+@pytest.mark.parametrize("b,s,hq,hkv", [(1, 2048, 24, 8), (8, 1, 24, 8), (16, 1, 32, 8),
+                                        (2, 37, 6, 2)])
+def test_rope_matches_oracle(dev, b, s, hq, hkv):
+    cos, sin = rope_tables(4096, 128, 500000.0)
+    q = torch.randn(b, s, hq, 128, generator=gen(b + s)).half()
+    k = torch.randn(b, s, hkv, 128, generator=gen(b * s + 1)).half()
+    pos = torch.randint(0, 4096, (b, s), generator=gen(3), dtype=torch.int32)
+    if s > 1:
+        pos = torch.arange(s, dtype=torch.int32).repeat(b, 1)
+    qd, kd = q.to(dev), k.to(dev)
+    ops.rope_inplace(qd, kd, cos.to(dev), sin.to(dev), pos.to(dev))
+    for got, x in ((qd.cpu(), q), (kd.cpu(), k)):
+        ref = rope_ref(x, cos, sin, pos)
+        ok, err = rel_close(got, ref, rel=4e-3, abs_=2e-3)
+        assert ok, err
+
+
+def test_rope_strided_views_and_no_key(dev):
+    """Q/K as views into a fused [B, S, (Hq + 2 Hkv) * D] projection."""
+    b, s, hq, hkv, d = 2, 9, 24, 8, 128
+    cos, sin = rope_tables(64, d, 500000.0)
+    fused = torch.randn(b, s, (hq + 2 * hkv) * d, generator=gen(4)).half()
+    fd = fused.to(dev)
+    qv = fd[..., : hq * d].view(b, s, hq, d)
+    kv = fd[..., hq * d:(hq + hkv) * d].view(b, s, hkv, d)
+    pos = torch.arange(s, dtype=torch.int32).repeat(b, 1) + 5
+    ops.rope_inplace(qv, kv, cos.to(dev), sin.to(dev), pos.to(dev))
+    got = fd.cpu()
+    q_ref = rope_ref(fused[..., : hq * d].view(b, s, hq, d), cos, sin, pos)
+    k_ref = rope_ref(fused[..., hq * d:(hq + hkv) * d].view(b, s, hkv, d), cos, sin, pos)
+    assert rel_close(got[..., : hq * d].view(b, s, hq, d), q_ref, 4e-3, 2e-3)[0]
+    assert rel_close(got[..., hq * d:(hq + hkv) * d].view(b, s, hkv, d), k_ref, 4e-3, 2e-3)[0]
+    assert torch.equal(got[..., (hq + hkv) * d:], fused[..., (hq + hkv) * d:])  # V untouched
+    q2 = torch.randn(1, 3, 4, d, generator=gen(5)).half()
+    q2d = q2.to(dev)
+    ops.rope_inplace(q2d, None, cos.to(dev), sin.to(dev), torch.tensor([[0, 1, 2]], dtype=torch.int32, device=dev))
+    assert rel_close(q2d.cpu(), rope_ref(q2, cos, sin, torch.tensor([[0, 1, 2]])), 4e-3, 2e-3)[0]
+
+
+def test_rope_out_of_table_positions_untouched(dev):
+    cos, sin = rope_tables(16, 128, 500000.0)
+    q = torch.randn(1, 4, 2, 128, generator=gen(6)).half()
+    k = torch.randn(1, 4, 1, 128, generator=gen(7)).half()
+    pos = torch.tensor([[3, 16, -1, 15]], dtype=torch.int32)
+    qd, kd = q.to(dev), k.to(dev)
+    ops.rope_inplace(qd, kd, cos.to(dev), sin.to(dev), pos.to(dev))
+    assert torch.equal(qd.cpu()[:, 1:3], q[:, 1:3]) and torch.equal(kd.cpu()[:, 1:3], k[:, 1:3])
+
+
+# ----------------------------------------------------------------- KV store
+@pytest.mark.parametrize("bs", [16, 8, 32])
+def test_kv_store_bit_exact(dev, bs):
+    n, hkv, d, nb = 300, 8, 128, 64
+    key = torch.randn(n, hkv, d, generator=gen(8)).half()
+    val = torch.randn(n, hkv, d, generator=gen(9)).half()
+    slots = torch.randperm(nb * bs, generator=gen(10))[:n].to(torch.int32)
+    slots[::7] = -1
+    slots[5] = nb * bs + 3  # past the pool: skipped
+    kc = torch.randn(nb, bs, hkv, d, generator=gen(11)).half()
+    vc = torch.randn(nb, bs, hkv, d, generator=gen(12)).half()
+    kcd, vcd = kc.to(dev), vc.to(dev)
+    ops.paged_kv_store(key.to(dev), val.to(dev), kcd, vcd, slots.to(dev))
+    kr, vr = kc.numpy().copy(), vc.numpy().copy()
+    kv_store_ref(key.numpy(), val.numpy(), kr, vr, slots.numpy())
+    assert torch.equal(kcd.cpu(), torch.from_numpy(kr))
+    assert torch.equal(vcd.cpu(), torch.from_numpy(vr))
+
+
+def test_kv_store_strided_token_views(dev):
+    """k[:, p] of a [B, S, Hkv, D] tensor, as the reference's prefill driver passes
+    (benchmarks/benchmark_engine.py:71-73); all S positions in one launch too."""
+    b, s, hkv, d, bs = 3, 20, 8, 128, 16
+    k = torch.randn(b, s, hkv, d, generator=gen(13)).half()
+    v = torch.randn(b, s, hkv, d, generator=gen(14)).half()
+    alloc = BlockAllocatorRef(16, bs)
+    for i in range(b):
+        alloc.allocate_sequence(i, s)
+    slots = torch.from_numpy(prefill_slots_ref(alloc.tables, list(range(b)), s, bs))
+    kc = torch.zeros(16, bs, hkv, d).half()
+    vc = torch.zeros(16, bs, hkv, d).half()
+    kcd, vcd = kc.clone().to(dev), vc.clone().to(dev)
+    kd, vd = k.to(dev), v.to(dev)
+    sl = slots.view(b, s)
+    for p in range(s):  # per-position views (token stride s * hkv * d)
+        ops.paged_kv_store(kd[:, p], vd[:, p], kcd, vcd, sl[:, p].contiguous().to(dev))
+    kcd2, vcd2 = kc.clone().to(dev), vc.clone().to(dev)
+    ops.paged_kv_store(kd.view(b * s, hkv, d), vd.view(b * s, hkv, d), kcd2, vcd2, slots.to(dev))
+    kr, vr = kc.numpy().copy(), vc.numpy().copy()
+    kv_store_ref(k.reshape(b * s, hkv, d).numpy(), v.reshape(b * s, hkv, d).numpy(), kr, vr,
+                 slots.numpy())
+    for got in (kcd.cpu(), kcd2.cpu()):
+        assert torch.equal(got, torch.from_numpy(kr))
+    for got in (vcd.cpu(), vcd2.cpu()):
+        assert torch.equal(got, torch.from_numpy(vr))
+
+
+# ------------------------------------------------------------ causal prefill
+@pytest.mark.parametrize("s", [1, 2, 17, 64, 127, 128, 129, 300, 512, 1000])
+@pytest.mark.parametrize("hq,hkv", [(24, 8), (4, 4), (6, 2)])
+def test_prefill_matches_oracle(dev, s, hq, hkv):
+    case = make_prefill_case(20 + s, 2 if s <= 512 else 1, s, hq, hkv)
+    out = ops.prefill_attention(case.query.to(dev), case.key.to(dev), case.value.to(dev),
+                                case.scale).cpu()
+    ref = prefill_attention_ref(case.query, case.key, case.value, case.scale)
+    assert not torch.isnan(out).any()
+    err = (out.float() - ref).abs().max().item()
+    assert err <= TOL, err
+
+
+def test_prefill_first_row_is_v0(dev):
+    case = make_prefill_case(30, 1, 200)
+    out = ops.prefill_attention(case.query.to(dev), case.key.to(dev), case.value.to(dev),
+                                case.scale).cpu()
+    v0 = case.value[0, 0].repeat_interleave(3, dim=0)
+    assert torch.equal(out[0, 0], v0)
+
+
+def test_cfg3_rope_kvstore_prefill_pipeline(dev):
+    """cfg3: RoPE (theta 5e5, positions 0..2047) in place, all 2048 K/V rows
+    into 16-token pages of a permuted table (bit-exact), then causal attention."""
+    case = cfg3_prefill()
+    b, s, hq, d = case.query.shape
+    hkv = case.key.shape[2]
+    cos, sin = rope_tables(4096, d, 500000.0)
+    pos = torch.arange(s, dtype=torch.int32).view(1, s)
+    q, k, v = case.query.to(dev), case.key.to(dev), case.value.to(dev)
+    ops.rope_inplace(q, k, cos.to(dev), sin.to(dev), pos.to(dev))
+    q_ref = rope_ref(case.query, cos, sin, pos)
+    k_ref = rope_ref(case.key, cos, sin, pos)
+    assert rel_close(q.cpu(), q_ref, 4e-3, 2e-3)[0] and rel_close(k.cpu(), k_ref, 4e-3, 2e-3)[0]
+    nb = 160
+    table = torch.randperm(nb, generator=gen(44))[: s // 16]
+    slots = (table.repeat_interleave(16) * 16 + torch.arange(s) % 16).to(torch.int32)
+    kc = torch.zeros(nb, 16, hkv, d, dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    ops.paged_kv_store(k[0], v[0], kc, vc, slots.to(dev))
+    kr = torch.zeros(nb, 16, hkv, d, dtype=torch.float16).numpy()
+    vr = kr.copy()
+    kv_store_ref(k[0].cpu().numpy(), v[0].cpu().numpy(), kr, vr, slots.numpy())
+    assert torch.equal(kc.cpu(), torch.from_numpy(kr)) and torch.equal(vc.cpu(), torch.from_numpy(vr))
+    out = ops.prefill_attention(q, k, v, case.scale).cpu()
+    ref = prefill_attention_ref(q.cpu(), k.cpu(), v.cpu(), case.scale)
+    err = (out.float() - ref).abs().max().item()
+    assert err <= TOL, err
