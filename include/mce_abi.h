@@ -92,9 +92,11 @@ MCE_API int mce_paged_kv_store(int dtype, const void *key, const void *value,
 
 /*
  * Workspace bytes mce_paged_attention_decode needs for these dimensions
- * (split-K partial softmax state).  Depends only on host-known sizes.
+ * (split-K partial softmax state).  Depends only on host-known sizes;
+ * 0 means no workspace is needed.
  */
 MCE_API size_t mce_paged_attention_decode_workspace_size(int batch, int num_heads,
+                                                 int num_kv_heads,
                                                  int max_blocks_per_seq,
                                                  int block_size);
 
@@ -111,6 +113,10 @@ MCE_API size_t mce_paged_attention_decode_workspace_size(int batch, int num_head
  * clamped into range (the reference reads out of bounds there).
  * head_dim must be 128, block_size a power of two in [8, 256],
  * num_heads / num_kv_heads in [1, 8].
+ * Workspace: 256-byte aligned, at least
+ * mce_paged_attention_decode_workspace_size() bytes, no initialisation
+ * needed; it is scratch for the duration of the call (two calls that run
+ * concurrently need two workspaces).
  * Replaces paged_attention_decode_cuda (csrc/kernels/flash_attn_paged.cu:
  * 144-168; binding csrc/bindings.cpp:8,26).
  */

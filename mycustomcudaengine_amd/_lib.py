@@ -39,7 +39,7 @@ SIGNATURES = {
     "mce_swiglu": (_c_int, [_c_int, _vp, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp]),
     "mce_paged_kv_store": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_i64, _c_int, _c_int,
                                     _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _vp]),
-    "mce_paged_attention_decode_workspace_size": (_c_sz, [_c_int, _c_int, _c_int, _c_int]),
+    "mce_paged_attention_decode_workspace_size": (_c_sz, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "mce_paged_attention_decode": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_int,
                                             _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64,
                                             _c_f, _vp, _c_sz, _vp]),

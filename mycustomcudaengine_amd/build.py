@@ -43,6 +43,8 @@ def compile_flags() -> list[str]:
         "-std=c++17",
         "-fPIC",
         "-fvisibility=hidden",
+        # 16-bit storage is read and written through wider vector types.
+        "-fno-strict-aliasing",
         "-Wall",
         "-Wno-unused-function",
         # Packed fp32 VALU ops are kept out of every kernel.

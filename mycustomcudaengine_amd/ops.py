@@ -188,12 +188,13 @@ def paged_attention_decode(query: torch.Tensor, key_cache: torch.Tensor,
     out = torch.empty_like(q)
     with _on_device(dev):
         lib = _lib.load()
-        ws_bytes = lib.mce_paged_attention_decode_workspace_size(b, hq, mb, bs) if b else 0
-        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev) if ws_bytes else None
+        ws_bytes = lib.mce_paged_attention_decode_workspace_size(b, hq, hkv, mb, bs) if b else 0
+        ws = torch.empty(ws_bytes + 256, dtype=torch.uint8, device=dev) if ws_bytes else None
+        ws_ptr = (ws.data_ptr() + 255) & ~255 if ws is not None else None
         _lib.call("mce_paged_attention_decode", code, q.data_ptr(), key_cache.data_ptr(),
                   value_cache.data_ptr(), block_tables.data_ptr(), context_lens.data_ptr(),
-                  out.data_ptr(), b, hq, hkv, d, mb, bs, nb, float(scale),
-                  ws.data_ptr() if ws is not None else None, ws_bytes, _stream(dev))
+                  out.data_ptr(), b, hq, hkv, d, mb, bs, nb, float(scale), ws_ptr, ws_bytes,
+                  _stream(dev))
     return out
 
 

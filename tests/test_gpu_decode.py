@@ -143,3 +143,22 @@ def test_rejects_bad_inputs(dev):
         ops.paged_attention_decode(q[..., :64].contiguous(), kc[..., :64].contiguous(),
                                    vc[..., :64].contiguous(), bt, cl, case.max_blocks, 16,
                                    case.scale)
+
+
+def test_workspace_reuse_across_shapes(dev):
+    """The split-K arrival counters live in a reused workspace and must be left
+    at zero by every call: alternate multi-chunk shapes and re-check each."""
+    cases = [make_decode_case(40, 4, [3000, 129, 2048, 4096]),
+             make_decode_case(41, 2, [9000, 700], max_blocks=1024),
+             make_decode_case(42, 8, [600] * 8)]
+    for rep in range(2):
+        for case in cases:
+            check(case, dev)
+
+
+def test_cfg2_repeat_calls_identical(dev):
+    """Back-to-back calls on the same inputs give bit-identical outputs."""
+    case = make_decode_case(43, 16, [4096, 1000, 300, 2500] * 4)
+    first = run_gpu(case, dev)
+    for _ in range(3):
+        assert torch.equal(run_gpu(case, dev), first)
