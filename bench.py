@@ -15,7 +15,9 @@ Extra fields on the same JSON line:
   model     Llama-3.2-3B random-init graph-replayed decode tok/s (when built).
   cpu_baseline  the CPU oracle on the same cfg2 inputs, on this host's cores.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only decode]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+                       [--only decode|prefill|splitk]
+(--only runs one workload; only the default run prints the full result line.)
 """
 from __future__ import annotations
 
@@ -168,12 +170,14 @@ def main() -> None:
 
     dev = torch.device("cuda:0")
     result = {}
-    log("generating cfg2 inputs")
-    case2 = cfg2_decode()
-    ms, nbytes, gbs, graph_ms = bench_decode(case2, dev, args.steps, args.warmup)
-    log(f"cfg2 decode: {ms * 1e3:.1f} us/step ({gbs:.1f} GB/s); as hipGraph replays "
-        f"{graph_ms * 1e3:.1f} us/step")
-    result["decode"] = (ms, nbytes, gbs, graph_ms)
+    case2 = None
+    if args.only in (None, "decode"):
+        log("generating cfg2 inputs")
+        case2 = cfg2_decode()
+        ms, nbytes, gbs, graph_ms = bench_decode(case2, dev, args.steps, args.warmup)
+        log(f"cfg2 decode: {ms * 1e3:.1f} us/step ({gbs:.1f} GB/s); as hipGraph replays "
+            f"{graph_ms * 1e3:.1f} us/step")
+        result["decode"] = (ms, nbytes, gbs, graph_ms)
 
     extra = {}
     if args.only in (None, "prefill"):
@@ -196,6 +200,10 @@ def main() -> None:
                            "gbs": round(kgbs, 1), "frac_of_hbm_peak": round(kgbs / HBM_PEAK_GBS, 4)}
         del case4
         torch.cuda.empty_cache()
+
+    if "decode" not in result:  # a single non-headline workload was asked for
+        print(json.dumps({"metric": METRIC, "only": args.only, **extra}), flush=True)
+        return
 
     cpu = None
     if not args.no_cpu:

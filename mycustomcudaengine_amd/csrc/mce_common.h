@@ -8,7 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 
-#include "../../include/mce_abi.h"
+#include "mce_abi.h"
 
 namespace mce {
 

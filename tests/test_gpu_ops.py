@@ -177,11 +177,13 @@ def test_prefill_matches_oracle(dev, s, hq, hkv):
 
 
 def test_prefill_first_row_is_v0(dev):
+    """Row 0 attends to key 0 only, so its output is v_0 up to one rounding of
+    p = exp2(s c - m c) (computed as one FMA) and of the fp16 store."""
     case = make_prefill_case(30, 1, 200)
     out = ops.prefill_attention(case.query.to(dev), case.key.to(dev), case.value.to(dev),
                                 case.scale).cpu()
-    v0 = case.value[0, 0].repeat_interleave(3, dim=0)
-    assert torch.equal(out[0, 0], v0)
+    v0 = case.value[0, 0].repeat_interleave(3, dim=0).float()
+    assert (out[0, 0].float() - v0).abs().max().item() <= 2e-3 * (1 + v0.abs().max().item())
 
 
 def test_cfg3_rope_kvstore_prefill_pipeline(dev):
