@@ -1,0 +1,137 @@
+"""CPU: the C-ABI library loads, exports every entry point include/mce_abi.h
+declares, and rejects bad arguments on the host before any device work.
+
+No test here launches a kernel: every call below fails validation (or is a
+pure size query), so it runs on a machine without a GPU.
+"""
+import ctypes
+
+import pytest
+import torch
+
+from mycustomcudaengine_amd import _lib
+
+HEADER_ENTRY_POINTS = {
+    "mce_last_error", "mce_abi_version", "mce_rmsnorm", "mce_swiglu",
+    "mce_paged_kv_store", "mce_paged_attention_decode_workspace_size",
+    "mce_paged_attention_decode", "mce_rope_inplace", "mce_prefill_attention",
+}
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_header_declares_the_six_ops_and_helpers():
+    assert set(_lib.header_symbols()) == HEADER_ENTRY_POINTS
+
+
+def test_library_exports_every_header_symbol(lib):
+    for name in _lib.header_symbols():
+        assert hasattr(lib, name), name
+    assert set(_lib.SIGNATURES) == HEADER_ENTRY_POINTS
+
+
+def test_single_hip_runtime_mapped(lib):
+    assert len(_lib._hip_runtimes_mapped()) <= 1
+
+
+def test_version(lib):
+    assert lib.mce_abi_version() >= 100
+
+
+def _err(lib):
+    return lib.mce_last_error().decode()
+
+
+def test_rmsnorm_validation(lib):
+    assert lib.mce_rmsnorm(7, None, None, None, 1, 8, 8, 8, 1e-5, None) == _lib.MCE_ERR_INVALID
+    assert "dtype" in _err(lib)
+    assert lib.mce_rmsnorm(0, None, None, None, 1, 0, 0, 0, 1e-5, None) == _lib.MCE_ERR_INVALID
+    assert lib.mce_rmsnorm(0, None, None, None, 2, 8, 4, 8, 1e-5, None) == _lib.MCE_ERR_INVALID
+    assert lib.mce_rmsnorm(0, None, None, None, 2, 8, 8, 8, 1e-5, None) == _lib.MCE_ERR_INVALID
+    assert "null" in _err(lib)
+    assert lib.mce_rmsnorm(0, None, None, None, 0, 8, 8, 8, 1e-5, None) == _lib.MCE_OK
+
+
+def test_swiglu_validation(lib):
+    assert lib.mce_swiglu(0, None, None, 2, 8, 15, 8, None) == _lib.MCE_ERR_INVALID
+    assert lib.mce_swiglu(0, None, None, 0, 8, 16, 8, None) == _lib.MCE_OK
+
+
+def test_kv_store_validation(lib):
+    assert lib.mce_paged_kv_store(0, None, None, None, None, None, 4, 8, 128, 16, 10,
+                                  1024, 128, 1024, 128, None) == _lib.MCE_ERR_INVALID
+    assert lib.mce_paged_kv_store(0, None, None, None, None, None, 0, 8, 128, 16, 10,
+                                  1024, 128, 1024, 128, None) == _lib.MCE_OK
+
+
+def _decode(lib, **kw):
+    args = dict(dtype=0, q=1 << 12, kc=1 << 12, vc=1 << 12, bt=1 << 12, cl=1 << 12,
+                out=1 << 12, B=2, Hq=24, Hkv=8, D=128, maxb=4, bs=16, nb=10, scale=0.088,
+                ws=None, ws_bytes=0, stream=None)
+    args.update(kw)
+    a = args
+    return lib.mce_paged_attention_decode(
+        a["dtype"], a["q"], a["kc"], a["vc"], a["bt"], a["cl"], a["out"], a["B"], a["Hq"],
+        a["Hkv"], a["D"], a["maxb"], a["bs"], a["nb"], a["scale"], a["ws"], a["ws_bytes"],
+        a["stream"])
+
+
+def test_decode_validation(lib):
+    assert _decode(lib, D=64) == _lib.MCE_ERR_INVALID and "head_dim" in _err(lib)
+    assert _decode(lib, Hq=20) == _lib.MCE_ERR_INVALID
+    assert _decode(lib, bs=12) == _lib.MCE_ERR_INVALID and "block_size" in _err(lib)
+    assert _decode(lib, bs=4) == _lib.MCE_ERR_INVALID
+    assert _decode(lib, Hq=80) == _lib.MCE_ERR_UNSUPPORTED  # GQA group 10
+    assert _decode(lib, dtype=1) == _lib.MCE_ERR_UNSUPPORTED
+    assert _decode(lib, q=None) == _lib.MCE_ERR_INVALID
+    assert _decode(lib, nb=0) == _lib.MCE_ERR_INVALID
+    assert _decode(lib) == _lib.MCE_ERR_WORKSPACE  # no workspace given
+    assert _decode(lib, B=0) == _lib.MCE_OK
+
+
+def test_decode_workspace_size(lib):
+    f = lib.mce_paged_attention_decode_workspace_size
+    assert f(0, 24, 8, 4, 16) == 0
+    small, big = f(1, 24, 8, 4, 16), f(32, 24, 8, 256, 16)
+    assert 0 < small < big
+    assert big % 256 == 0
+
+
+def test_rope_and_prefill_validation(lib):
+    assert lib.mce_rope_inplace(0, None, None, None, None, None, 1, 1, 2, 1, 7, 16,
+                                0, 0, 0, 0, 0, 0, None) == _lib.MCE_ERR_INVALID
+    assert lib.mce_rope_inplace(0, None, None, None, None, None, 0, 1, 2, 1, 8, 16,
+                                0, 0, 0, 0, 0, 0, None) == _lib.MCE_OK
+    assert lib.mce_prefill_attention(0, None, None, None, None, 1, 8, 24, 8, 64, 0.1,
+                                     None) == _lib.MCE_ERR_INVALID
+    assert lib.mce_prefill_attention(0, None, None, None, None, 1, 8, 24, 7, 128, 0.1,
+                                     None) == _lib.MCE_ERR_INVALID
+    assert lib.mce_prefill_attention(0, None, None, None, None, 0, 8, 24, 8, 128, 0.1,
+                                     None) == _lib.MCE_OK
+
+
+def test_python_ops_reject_cpu_tensors():
+    import my_cuda_engine_cpp as ops
+    x = torch.zeros(2, 8, dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        ops.rmsnorm(x, torch.ones(8, dtype=torch.float16), 1e-5)
+    with pytest.raises(RuntimeError):
+        ops.swiglu(x)
+    q = torch.zeros(1, 24, 128, dtype=torch.float16)
+    kc = torch.zeros(4, 16, 8, 128, dtype=torch.float16)
+    with pytest.raises(RuntimeError):
+        ops.paged_attention_decode(q, kc, kc, torch.zeros(1, 4, dtype=torch.int32),
+                                   torch.ones(1, dtype=torch.int32), 4, 16, 0.088)
+    with pytest.raises(RuntimeError):
+        ops.prefill_attention(torch.zeros(1, 4, 24, 128, dtype=torch.float16),
+                              torch.zeros(1, 4, 8, 128, dtype=torch.float16),
+                              torch.zeros(1, 4, 8, 128, dtype=torch.float16), 0.088)
+
+
+def test_error_exception_carries_status(lib):
+    with pytest.raises(_lib.MCEError) as ei:
+        _lib.call("mce_rmsnorm", 9, None, None, None, 1, 8, 8, 8, 1e-5, None)
+    assert ei.value.code == _lib.MCE_ERR_INVALID and isinstance(ei.value, RuntimeError)
