@@ -1,0 +1,52 @@
+"""Batched prompt prefill (reference: benchmarks/benchmark_engine.py:12-129).
+
+prefill_step(model, input_ids [B, S], seq_ids, context_lens) -> last-token
+logits [B, vocab].  Per layer: RMSNorm -> fused q/k/v projection -> RoPE in
+place (positions 0..S-1) -> paged KV store of all B*S tokens in ONE launch ->
+causal prefill attention on the contiguous q/k/v -> o_proj + residual ->
+RMSNorm -> fused gate/up -> SwiGLU -> down + residual; then the final
+RMSNorm and lm_head on the last position only (benchmark_engine.py:124-127).
+
+Differences from the reference driver, all defects of it (not semantics):
+the reference builds slot_mapping element by element and launches the KV
+store once per position (benchmark_engine.py:64-73), reorders the attention
+output with a stray transpose (:90-91) and computes an unused GQA expansion
+(:79-87).  Here slots for every (sequence, position) come from the block
+tables in one host->device copy and the attention output is used as
+[B, S, Hq * D] directly.  The sequences must already own blocks for S tokens
+(KVCacheManager.allocate_sequence), as in the reference.
+"""
+from __future__ import annotations
+
+from typing import List
+
+import torch
+
+import my_cuda_engine_cpp as ops
+
+
+def prefill_step(model, input_ids: torch.Tensor, seq_ids: List[int],
+                 context_lens: torch.Tensor = None) -> torch.Tensor:
+    c = model.config
+    b, s = input_ids.shape
+    hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+    dev = input_ids.device
+    cache = model.cache_manager
+    slots = torch.from_numpy(cache.prefill_slot_mapping(seq_ids, s)).to(dev)
+    positions = torch.arange(s, dtype=torch.int32, device=dev).repeat(b, 1).contiguous()
+    x = model.weights["model.embed_tokens.weight"][input_ids.reshape(-1)]  # [B*S, hidden]
+    kv = cache.kv_cache
+    for l in range(c.num_hidden_layers):
+        p = f"model.layers.{l}"
+        xn = ops.rmsnorm(x, model.weights[f"{p}.input_layernorm.weight"], c.rms_norm_eps)
+        q, k, v = model._attention_block_proj(l, xn)
+        q4, k4, v4 = q.view(b, s, hq, d), k.view(b, s, hkv, d), v.view(b, s, hkv, d)
+        ops.rope_inplace(q4, k4, model.cos_table, model.sin_table, positions)
+        ops.paged_kv_store(k.view(b * s, hkv, d), v.view(b * s, hkv, d), kv[l, 0], kv[l, 1], slots)
+        attn = ops.prefill_attention(q4, k4, v4, model.scale)  # [B, S, Hq, D]
+        x = x + torch.matmul(attn.view(b * s, hq * d),
+                             model.weights[f"{p}.self_attn.o_proj.weight"].T)
+        x = model._mlp(l, x)
+    last = x.view(b, s, -1)[:, -1].contiguous()
+    xf = ops.rmsnorm(last, model.weights["model.norm.weight"], c.rms_norm_eps)
+    return torch.matmul(xf, model.lm_head.T)

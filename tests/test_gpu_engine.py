@@ -1,0 +1,113 @@
+"""GPU: the engine end to end on a 2-layer model with Llama-3.2-3B layer
+geometry (hidden 3072, 24/8 heads, head_dim 128, SwiGLU 8192) and a small
+vocabulary, against the fp32 CPU model oracle (oracle/model_ref.py).
+
+Bars: prefill and decode logits within a relative L2 error of 1e-2 and
+max-abs 5e-2 of the fp32 oracle (fp16 activations through 2 layers); the
+graph-replayed decode step equals the eager decode step within the
+reference's allclose(1e-2, 1e-2) (tests/test_cuda_graph.py:138); token ids,
+slots and block tables handled exactly (greedy tokens identical).
+"""
+import pytest
+import torch
+
+from mycustomcudaengine_amd.engine import (CUDAGraphRunner, KVCacheManager, Llama3BConfig,
+                                           Llama3BEngineModel, prefill_step)
+from oracle.model_ref import LlamaRef, random_llama_weights
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(hidden_size=3072, intermediate_size=8192, num_hidden_layers=2,
+           num_attention_heads=24, num_key_value_heads=8, head_dim=128, vocab_size=4096,
+           rms_norm_eps=1e-5, rope_theta=500000.0, max_position_embeddings=4096)
+
+
+def build(dev, batch, prompt, gen, seed=5, tied=True):
+    w_cpu = random_llama_weights(CFG, seed=seed, tied=tied)
+    weights = {k: v.to(dev) for k, v in w_cpu.items()}
+    cache = KVCacheManager(num_blocks=batch * ((prompt + gen + 15) // 16) + 8, block_size=16,
+                           num_layers=CFG["num_hidden_layers"], num_heads=8, head_dim=128,
+                           device=dev)
+    model = Llama3BEngineModel(Llama3BConfig(CFG), weights, cache)
+    for s in range(batch):
+        cache.allocate_sequence(s, prompt + gen)
+    return model, cache, LlamaRef(CFG, w_cpu)
+
+
+def close(gpu, ref, rel=1e-2, abs_=5e-2):
+    g = gpu.float().cpu()
+    err = (g - ref).norm() / ref.norm()
+    mx = (g - ref).abs().max().item()
+    assert err.item() <= rel and mx <= abs_, (err.item(), mx)
+
+
+def test_prefill_then_eager_decode_match_oracle(dev):
+    b, s = 2, 37
+    model, cache, ref = build(dev, b, s, 4, tied=False)
+    ids = torch.randint(0, CFG["vocab_size"], (b, s), generator=torch.Generator().manual_seed(1))
+    logits = prefill_step(model, ids.to(dev), [0, 1], torch.full((b,), s, dtype=torch.int32))
+    close(logits, ref.prefill(ids, [0, 1]))
+    tok = logits.argmax(-1, keepdim=True)
+    for i in range(3):
+        pos = s + i
+        slots = torch.from_numpy(cache.slot_mapping([0, 1], [pos + 1] * b)).to(dev)
+        mb = len(cache.block_tables[0])
+        bt = cache.get_block_table_tensor([0, 1], mb)
+        out = model.decode_step(tok, torch.full((b, 1), pos, dtype=torch.int32, device=dev),
+                                torch.full((b,), pos + 1, dtype=torch.int32, device=dev),
+                                slots, bt, mb)
+        want = ref.decode(tok.cpu(), [pos] * b, [0, 1])
+        close(out, want)
+        tok = want.argmax(-1, keepdim=True).to(dev)  # follow the oracle's greedy path
+
+
+def test_graph_replay_matches_eager(dev):
+    b, s, steps = 3, 20, 6
+    model, cache, _ = build(dev, b, s, steps + 1, seed=6)
+    seq = list(range(b))
+    ids = torch.randint(0, CFG["vocab_size"], (b, s), generator=torch.Generator().manual_seed(2))
+    logits = prefill_step(model, ids.to(dev), seq)
+    tok = logits.argmax(-1, keepdim=True)
+    runner = CUDAGraphRunner(model, max_batch_size=b)
+    ctx = torch.full((b,), s + 1, dtype=torch.int32, device=dev)
+    pos = torch.full((b, 1), s, dtype=torch.int32, device=dev)
+    runner.capture_graph(tok, pos, seq, ctx)
+    assert runner.max_blocks_per_seq == len(cache.block_tables[0])  # capacity, not ctx
+    for i in range(steps):
+        p = s + i
+        ctx = torch.full((b,), p + 1, dtype=torch.int32, device=dev)
+        pos = torch.full((b, 1), p, dtype=torch.int32, device=dev)
+        # eager first: both write the same K/V slot, so the graph sees the same cache
+        slots, bt, mb = runner._prepare_inputs(seq, ctx, max_blocks=runner.max_blocks_per_seq)
+        eager = model.decode_step(tok, pos, ctx, slots, bt, mb).clone()
+        graph = runner.execute(tok, pos, seq, ctx).clone()
+        torch.cuda.synchronize()
+        assert torch.allclose(graph.float(), eager.float(), atol=1e-2, rtol=1e-2), i
+        assert torch.equal(graph.argmax(-1), eager.argmax(-1))
+        tok = graph.argmax(-1, keepdim=True)
+
+
+def test_decode_crosses_block_boundary_and_block_table_width(dev):
+    """Decode past several 16-token blocks with the graph captured at the first
+    step (the reference would read past its frozen table width here)."""
+    b, s, steps = 2, 14, 40
+    model, cache, ref = build(dev, b, s, steps + 1, seed=7)
+    seq = [0, 1]
+    ids = torch.randint(0, CFG["vocab_size"], (b, s), generator=torch.Generator().manual_seed(3))
+    logits = prefill_step(model, ids.to(dev), seq)
+    ref.prefill(ids, seq)
+    tok = logits.argmax(-1, keepdim=True)
+    runner = CUDAGraphRunner(model, max_batch_size=b)
+    runner.capture_graph(tok, torch.full((b, 1), s, dtype=torch.int32, device=dev), seq,
+                         torch.full((b,), s + 1, dtype=torch.int32))
+    for i in range(steps):
+        p = s + i
+        out = runner.execute(tok, torch.full((b, 1), p, dtype=torch.int32, device=dev), seq,
+                             torch.full((b,), p + 1, dtype=torch.int32))
+        if i % 13 == 0 or i == steps - 1:
+            want = ref.decode(tok.cpu(), [p] * b, seq)
+            close(out, want)
+            tok = want.argmax(-1, keepdim=True).to(dev)
+        else:
+            ref.decode(tok.cpu(), [p] * b, seq)  # keep the oracle's cache in step
+            tok = out.argmax(-1, keepdim=True)
