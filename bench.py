@@ -12,7 +12,8 @@ Extra fields on the same JSON line:
   prefill   cfg3 causal prefill (S=2048, 24/8 heads): algorithmic TFLOP/s
             (2 * D * Hq * S * (S+1)) and fraction of dense fp16 MFMA peak.
   splitk    cfg4 long-context decode (B=8, ctx 32768): GB/s.
-  model     Llama-3.2-3B random-init graph-replayed decode tok/s (when built).
+  model     cfg5 Llama-3.2-3B random-init, B=8, prefill 512 then 128 greedy
+            decode steps replayed via hipGraph: tok/s, ms/step, TTFT.
   cpu_baseline  the CPU oracle on the same cfg2 inputs, on this host's cores.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
@@ -31,6 +32,8 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor spec
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "decode_hbm_traffic.json")
 FP16_DENSE_TFLOPS = 2500.0     # MI355X dense fp16 MFMA, vendor spec
 METRIC = "decode-attn HBM GB/s (% peak); prefill-attn TFLOPS (% MFMA); 3B decode tok/s"
 
@@ -120,6 +123,93 @@ def bench_prefill(case, dev, steps, warmup):
     return ms, flops, flops / (ms * 1e-3) / 1e12
 
 
+def bench_model(dev, steps: int = 128, batch: int = 8, prompt: int = 512, seed: int = 46) -> dict:
+    """cfg5: random-init Llama-3.2-3B (28 layers, fp16 weights ~ N(0, 0.02),
+    RMSNorm weights 1, tied lm_head), B=8 prefill of 512 uniform-random token
+    ids, then `steps` greedy decode steps replayed through the hipGraph runner.
+    tok/s = B * steps / wall time of the decode loop (host preparation of
+    slots/tables included, no per-step synchronisation)."""
+    from mycustomcudaengine_amd.engine import (CUDAGraphRunner, KVCacheManager, Llama3BConfig,
+                                               Llama3BEngineModel, prefill_step)
+    cfg = Llama3BConfig({})
+    g = torch.Generator(device=dev).manual_seed(seed)
+    h, inter, d = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+    hq, hkv = cfg.num_attention_heads, cfg.num_key_value_heads
+
+    def rnd(*shape):
+        return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * 0.02).half()
+
+    w = {"model.embed_tokens.weight": rnd(cfg.vocab_size, h),
+         "model.norm.weight": torch.ones(h, dtype=torch.float16, device=dev)}
+    for l in range(cfg.num_hidden_layers):
+        p = f"model.layers.{l}"
+        w[f"{p}.input_layernorm.weight"] = torch.ones(h, dtype=torch.float16, device=dev)
+        w[f"{p}.post_attention_layernorm.weight"] = torch.ones(h, dtype=torch.float16, device=dev)
+        w[f"{p}.self_attn.q_proj.weight"] = rnd(hq * d, h)
+        w[f"{p}.self_attn.k_proj.weight"] = rnd(hkv * d, h)
+        w[f"{p}.self_attn.v_proj.weight"] = rnd(hkv * d, h)
+        w[f"{p}.self_attn.o_proj.weight"] = rnd(h, hq * d)
+        w[f"{p}.mlp.gate_proj.weight"] = rnd(inter, h)
+        w[f"{p}.mlp.up_proj.weight"] = rnd(inter, h)
+        w[f"{p}.mlp.down_proj.weight"] = rnd(h, inter)
+    weight_bytes = sum(t.numel() * t.element_size() for t in w.values())
+    total = prompt + steps + 1
+    blocks_per_seq = (total + 15) // 16
+    cache = KVCacheManager(batch * blocks_per_seq + 16, 16, cfg.num_hidden_layers, hkv, d,
+                           device=dev)
+    model = Llama3BEngineModel(cfg, w, cache)
+    seq = list(range(batch))
+    for s in seq:
+        cache.allocate_sequence(s, total)
+    ids = torch.randint(0, cfg.vocab_size, (batch, prompt), generator=g, device=dev)
+    prefill_step(model, ids, seq)  # warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    logits = prefill_step(model, ids, seq)
+    torch.cuda.synchronize()
+    ttft_ms = (time.perf_counter() - t0) * 1e3
+    tok = logits.argmax(-1, keepdim=True)
+    runner = CUDAGraphRunner(model, max_batch_size=batch)
+    runner.capture_graph(tok, torch.full((batch, 1), prompt, dtype=torch.int32, device=dev), seq,
+                         [prompt + 1] * batch)
+    pos_buf = torch.empty((batch, 1), dtype=torch.int32, device=dev)
+    # per-step latency with a sync around each step (the reference's ITL)
+    itl = []
+    for i in range(8):
+        p = prompt + i
+        pos_buf.fill_(p)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        out = runner.execute(tok, pos_buf, seq, [p + 1] * batch)
+        torch.cuda.synchronize()
+        itl.append((time.perf_counter() - t1) * 1e3)
+        tok = out.argmax(-1, keepdim=True)
+    # throughput: `steps` back-to-back graph replays with greedy feedback on device
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for i in range(steps):
+        p = prompt + i
+        pos_buf.fill_(p)
+        out = runner.execute(tok, pos_buf, seq, [p + 1] * batch)
+        tok = out.argmax(-1, keepdim=True)
+    torch.cuda.synchronize()
+    loop_s = time.perf_counter() - t1
+    step_ms = loop_s / steps * 1e3
+    mean_ctx = prompt + steps / 2
+    kv_bytes = batch * mean_ctx * cfg.num_hidden_layers * hkv * d * 2 * 2
+    return {"workload": "cfg5 Llama-3.2-3B random-init fp16, B=8, prefill 512, "
+                        f"{steps} greedy decode steps replayed via hipGraph",
+            "tok_s": round(batch * steps / loop_s, 1),
+            "steps_per_s": round(steps / loop_s, 2),
+            "ms_per_step": round(step_ms, 4),
+            "itl_ms_synced": round(sorted(itl)[len(itl) // 2], 4),
+            "ttft_ms": round(ttft_ms, 2),
+            "bytes_per_step": int(weight_bytes + kv_bytes),
+            "gbs": round((weight_bytes + kv_bytes) / (step_ms * 1e-3) / 1e9, 1),
+            "frac_of_hbm_peak": round((weight_bytes + kv_bytes) / (step_ms * 1e-3) / 1e9
+                                      / HBM_PEAK_GBS, 4)}
+
+
 def cpu_baseline_decode(case) -> dict:
     """The CPU oracle (fp32, torch on this host's cores) on the same inputs."""
     from oracle.ops_ref import decode_attention_ref
@@ -147,13 +237,27 @@ def cpu_baseline_decode(case) -> dict:
                       f"{med * 1e3:.1f} ms/run; {info['cpu_model']}; torch {info['torch']}"}
 
 
+def measured_traffic():
+    """HBM bytes per decode-kernel launch from the committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE passes (calibrated against a 256 MiB copy), or None
+    when that summary is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return int(json.load(f)["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "prefill", "splitk"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "splitk", "model"], default=None)
+    ap.add_argument("--calibration-copy", action="store_true",
+                    help="first copy 256 MiB device-to-device (a kernel of known traffic, "
+                         "used to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not "
@@ -169,6 +273,13 @@ def main() -> None:
     from oracle.inputs import cfg2_decode, cfg3_prefill, cfg4_decode
 
     dev = torch.device("cuda:0")
+    if args.calibration_copy:
+        src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     result = {}
     case2 = None
     if args.only in (None, "decode"):
@@ -201,6 +312,12 @@ def main() -> None:
         del case4
         torch.cuda.empty_cache()
 
+    if args.only in (None, "model"):
+        log("cfg5 Llama-3.2-3B decode")
+        extra["model"] = bench_model(dev)
+        log(f"cfg5 model: {extra['model']['tok_s']} tok/s, {extra['model']['ms_per_step']} ms/step")
+        torch.cuda.empty_cache()
+
     if "decode" not in result:  # a single non-headline workload was asked for
         print(json.dumps({"metric": METRIC, "only": args.only, **extra}), flush=True)
         return
@@ -230,7 +347,8 @@ def main() -> None:
                    "batch": 32, "tokens": int(case2.context_lens.sum()),
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "timing": {"method": "K back-to-back op calls from Python (decode kernel + LSE "
                              "merge kernel each), HIP events on the launch stream",
