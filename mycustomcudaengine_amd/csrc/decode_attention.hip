@@ -31,15 +31,16 @@
 // Per wave and 32-token tile, with the next tile's K/V loads in flight while
 // the current tile is computed:
 //   * the segment's physical block ids are staged in LDS;
-//   * K^T tile -> MFMA B operand straight from global memory: lane l loads
-//     token (l % 16) of each 16-token half, 4 x 16 bytes, so one instruction
-//     covers 64 contiguous bytes of 16 token rows.
-//     S = Q K^T with v_mfma_f32_16x16x32_f16, A = Q (rows = query heads,
-//     zero-padded to 16).  S row h lands in lane group h / 4, register h % 4.
-//   * online softmax in base 2 (scale * log2 e folded in).
-//   * p goes through a small LDS slice as packed fp16 token pairs; V rows are
-//     read as 16-byte pieces (16 lanes cover one 256-byte token row, 4 rows
-//     per instruction) and accumulated with v_dot2_f32_f16 over token pairs.
+//   * lane group lg (16 lanes) owns tokens 8 lg .. 8 lg + 7 of the tile and
+//     lane lr owns dims 8 lr .. 8 lr + 7: every K and V load instruction reads
+//     four whole 256-byte token rows (the pattern that streams fastest on
+//     MI355X; loading K in an MFMA-operand layout, 64-byte pieces of 16 rows
+//     per instruction, measured ~6% slower);
+//   * scores: v_dot2_f32_f16 over the lane's dims and a 16-lane DPP sum, so
+//     every lane of a group holds its tokens' scores for all G query heads;
+//   * online softmax in base 2 (p = exp2((s - m) c), c = scale log2 e);
+//   * P V with v_dot2_f32_f16 over token pairs, from the same registers --
+//     no LDS round trip for p.
 #include "mce_common.h"
 
 namespace mce {
@@ -138,8 +139,6 @@ void paged_decode_kernel(DecodeArgs a) {
   __shared__ int pre[MAX_BATCH + 1];
   __shared__ int wave_tot[DEC_NW];
   __shared__ int blk_lds[MAX_IDS];
-  // p of one tile as packed fp16 token pairs: [wave][head][pair / 4][pair % 4]
-  __shared__ u32x4 p_lds[DEC_NW][G][TILE / 8];
   __shared__ float red_acc[DEC_NW][G][HD];
   __shared__ float red_m[DEC_NW][G], red_l[DEC_NW][G];
 
@@ -189,29 +188,27 @@ void paged_decode_kernel(DecodeArgs a) {
     const int j_first = owner_of(pre[b], NT, je);
     const int nparts = owner_of(pre[b + 1] - 1, NT, je) - j_first + 1;
 
-    // Q as MFMA A operand: row = query head lr, k-piece (4i + lg) = dims
-    // [8(4i+lg), 8(4i+lg)+8).  The same piece mapping is used for K below.
-    half8 qa[4];
+    // This lane's slice of each query head: dims 8 lr .. 8 lr + 7 as packed
+    // fp16 pairs -- the same dims the lane loads from every K and V row.
+    u32x4 qv[G];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (active && lr < G) {
-        const uint16_t *qp =
-            a.query + ((int64_t)b * a.Hq + head0 + lr) * HD + (4 * i + lg) * 8;
-        qa[i] = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4 *>(qp));
-      } else {
-        qa[i] = half8{0, 0, 0, 0, 0, 0, 0, 0};
-      }
-    }
+    for (int h = 0; h < G; ++h)
+      qv[h] = active ? *reinterpret_cast<const u32x4 *>(
+                           a.query + ((int64_t)b * a.Hq + head0 + h) * HD + lr * 8)
+                     : u32x4{0, 0, 0, 0};
 
-    float m_run[G], l_part[4], acc[G][8];
+    // m_run: running max of the raw scores (uniform over the wave);
+    // l_grp: softmax denominator of this lane group's tokens;
+    // acc:   unnormalised output, dims 8 lr .. 8 lr + 7, this group's tokens.
+    float m_run[G], l_grp[G], acc[G][8];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       m_run[h] = -INFINITY;
+      l_grp[h] = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
     }
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) l_part[jj] = 0.f;
+    const float c = a.scale_log2;
 
     const int32_t *bt = a.btab + (int64_t)b * a.maxb;
     // Sub-ranges of the segment whose block ids fit in LDS (one for every
@@ -229,88 +226,67 @@ void paged_decode_kernel(DecodeArgs a) {
       __syncthreads();
       if (!active) continue;
 
-      auto slot_of = [&](int t) -> int64_t {
-        const int64_t phys = blk_lds[(t >> bs_log2) - first_blk];
-        return (phys << bs_log2) + (t & (bs - 1));
-      };
-      // ---- loads of one tile into registers ----
-      auto load_tile = [&](int t0, half8 (&kb)[2][4], u32x4 (&vv)[8]) {
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          int t = t0 + 16 * u + lr;
-          t = t < t_end ? t : t_end - 1;
-          const uint16_t *kp = kbase + slot_of(t) * slot_stride + lg * 8;
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            kb[u][i] = __builtin_bit_cast(half8, ld_nt(kp + i * 32));
-        }
-        // lane group lg owns tokens t0 + 8 lg .. +7 (one block: bs >= 8)
+      // ---- loads of one tile: lane group lg owns tokens t0 + 8 lg .. +7 (one
+      // block, since bs >= 8); each K and V row is one 256-byte run read by
+      // 16 lanes x 16 bytes ----
+      auto load_tile = [&](int t0, u32x4 (&kk)[8], u32x4 (&vv)[8]) {
         int tv = t0 + 8 * lg;
         tv = tv < t_end ? tv : t0;
-        const uint16_t *vp = vbase + slot_of(tv) * slot_stride + lr * 8;
+        const int64_t phys = blk_lds[(tv >> bs_log2) - first_blk];
+        const int64_t off = ((phys << bs_log2) + (tv & (bs - 1))) * slot_stride + lr * 8;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) vv[s] = ld_nt(vp + s * slot_stride);
+        for (int s8 = 0; s8 < 8; ++s8) kk[s8] = ld_nt(kbase + off + s8 * slot_stride);
+#pragma unroll
+        for (int s8 = 0; s8 < 8; ++s8) vv[s8] = ld_nt(vbase + off + s8 * slot_stride);
       };
       // ---- compute of one tile ----
-      auto compute_tile = [&](int t0, const half8 (&kb)[2][4], u32x4 (&vv)[8]) {
-        floatx4 sacc[2];
+      auto compute_tile = [&](int t0, const u32x4 (&kk)[8], u32x4 (&vv)[8]) {
+        const int tv = t0 + 8 * lg;
+        // scores: 4 v_dot2 over the lane's 8 dims, then a 16-lane DPP sum;
+        // every lane of a group ends with the scores of the group's 8 tokens
+        float sc[8][G];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          sacc[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int s8 = 0; s8 < 8; ++s8)
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            sacc[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[i], kb[u][i],
-                                                             sacc[u], 0, 0, 0);
-        }
-        float s[2][4];
+          for (int h = 0; h < G; ++h) {
+            float d = 0.f;
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const bool valid = t0 + 16 * u + lr < t_end;
-#pragma unroll
-          for (int jj = 0; jj < 4; ++jj)
-            s[u][jj] = valid ? sacc[u][jj] * a.scale_log2 : -INFINITY;
-        }
-        float mx[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) mx[jj] = row16_max(fmaxf(s[0][jj], s[1][jj]));
-
+            for (int k = 0; k < 4; ++k)
+              // (explicit conversions: bit_cast of an ext-vector element picks
+              // element 0 in this compiler)
+              d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, (uint32_t)kk[s8][k]),
+                                         __builtin_bit_cast(h2, (uint32_t)qv[h][k]), d, false);
+            d = row16_sum(d);
+            sc[s8][h] = tv + s8 < t_end ? d : -INFINITY;
+          }
+        // online softmax in base 2: p = exp2(s c - m c)
         float alpha[G];
         bool rescale = false;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          const float tmax = __builtin_bit_cast(
-              float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mx[h & 3]),
-                                               16 * (h >> 2)));
-          const float mn = fmaxf(m_run[h], tmax);
-          alpha[h] = fast_exp2(m_run[h] - mn);
+          float mx = fmaxf(fmaxf(fmaxf(sc[0][h], sc[1][h]), fmaxf(sc[2][h], sc[3][h])),
+                           fmaxf(fmaxf(sc[4][h], sc[5][h]), fmaxf(sc[6][h], sc[7][h])));
+          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          mx = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, mx)));
+          const float mn = fmaxf(m_run[h], mx);
+          alpha[h] = fast_exp2((m_run[h] - mn) * c);
           rescale |= mn != m_run[h];
           m_run[h] = mn;
         }
-        // p for the head held in register jj of this lane (head 4 lg + jj)
+        float p[8][G];
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          float mj = 0.f, al = 1.f;
+        for (int h = 0; h < G; ++h) {
+          // (s - m) c rather than one FMA: exactly 0 at the max, so a single
+          // token gets p = 1 and the output is v itself
+          float ps = 0.f;
 #pragma unroll
-          for (int h = 0; h < G; ++h)
-            if ((h & 3) == jj && lg == (h >> 2)) {
-              mj = m_run[h];
-              al = alpha[h];
-            }
-          const float p0 = fast_exp2(s[0][jj] - mj), p1 = fast_exp2(s[1][jj] - mj);
-          l_part[jj] = l_part[jj] * al + p0 + p1;
-          // even lanes store (p[t], p[t + 1]) for tokens t = lr and 16 + lr
-          const float p0n = dpp_f<0xB1>(p0), p1n = dpp_f<0xB1>(p1);
-          const int h = 4 * lg + jj;
-          if (h < G && (lr & 1) == 0) {
-            const int pair = lr >> 1;
-            p_lds[w][h][pair >> 2][pair & 3] = pack2<F16T>(p0, p0n);
-            p_lds[w][h][2 + (pair >> 2)][pair & 3] = pack2<F16T>(p1, p1n);
+          for (int s8 = 0; s8 < 8; ++s8) {
+            p[s8][h] = fast_exp2((sc[s8][h] - m_run[h]) * c);
+            ps += p[s8][h];
           }
+          l_grp[h] = l_grp[h] * alpha[h] + ps;
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
         if (rescale) {
 #pragma unroll
           for (int h = 0; h < G; ++h)
@@ -318,16 +294,16 @@ void paged_decode_kernel(DecodeArgs a) {
             for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
         }
         // tokens past the end: zero their V rows (p is 0, V may be NaN garbage)
-        const int tv = t0 + 8 * lg;
 #pragma unroll
         for (int s8 = 0; s8 < 8; ++s8)
           if (tv + s8 >= t_end) vv[s8] = u32x4{0, 0, 0, 0};
-        // ---- acc += P V over token pairs with v_dot2_f32_f16 ----
-        u32x4 pr[G];
+        // acc += P V over token pairs with v_dot2_f32_f16
 #pragma unroll
-        for (int h = 0; h < G; ++h) pr[h] = p_lds[w][h][lg];
+        for (int sp = 0; sp < 4; ++sp) {
+          h2 pp[G];
 #pragma unroll
-        for (int sp = 0; sp < 4; ++sp)
+          for (int h = 0; h < G; ++h)
+            pp[h] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(p[2 * sp][h], p[2 * sp + 1][h]));
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             const h2 lo = __builtin_bit_cast(
@@ -336,20 +312,16 @@ void paged_decode_kernel(DecodeArgs a) {
                 h2, __builtin_amdgcn_perm(vv[2 * sp + 1][k], vv[2 * sp][k], 0x07060302u));
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-              // (explicit conversion: bit_cast of an ext-vector element picks
-              // element 0 in this compiler)
-              const h2 ph = __builtin_bit_cast(h2, (uint32_t)pr[h][sp]);
-              acc[h][2 * k] = __builtin_amdgcn_fdot2(lo, ph, acc[h][2 * k], false);
-              acc[h][2 * k + 1] = __builtin_amdgcn_fdot2(hi, ph, acc[h][2 * k + 1], false);
+              acc[h][2 * k] = __builtin_amdgcn_fdot2(lo, pp[h], acc[h][2 * k], false);
+              acc[h][2 * k + 1] = __builtin_amdgcn_fdot2(hi, pp[h], acc[h][2 * k + 1], false);
             }
           }
-        __builtin_amdgcn_wave_barrier();
+        }
       };
 
       // ---- software-pipelined tile loop: next tile's loads before compute ----
       const int ntile = (t_end - s_lo + TILE - 1) / TILE;
-      half8 kA[2][4], kB[2][4];
-      u32x4 vA[8], vB[8];
+      u32x4 kA[8], kB[8], vA[8], vB[8];
       int k = rlane;
       if (k < ntile) load_tile(s_lo + TILE * k, kA, vA);
       while (k < ntile) {
@@ -365,24 +337,22 @@ void paged_decode_kernel(DecodeArgs a) {
       }
     }
 
-    // ---- per-wave reduction ----
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) l_part[jj] = row16_sum(l_part[jj]);
+    // ---- per-wave reduction over the four lane groups ----
     float l_tot[G];
 #pragma unroll
-    for (int h = 0; h < G; ++h)
-      l_tot[h] = __builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, l_part[h & 3]),
-                                           16 * (h >> 2)));
-#pragma unroll
-    for (int h = 0; h < G; ++h)
+    for (int h = 0; h < G; ++h) {
+      float v = l_grp[h];
+      v += __shfl_xor(v, 16, 64);
+      v += __shfl_xor(v, 32, 64);
+      l_tot[h] = v;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        float v = acc[h][e];
-        v += __shfl_xor(v, 16, 64);
-        v += __shfl_xor(v, 32, 64);
-        acc[h][e] = v;
+        float x = acc[h][e];
+        x += __shfl_xor(x, 16, 64);
+        x += __shfl_xor(x, 32, 64);
+        acc[h][e] = x;
       }
+    }
     const int64_t row0 = (int64_t)b * a.Hq + head0;
     const int slot = j - j_first;
     if (wph == 1) {
@@ -406,7 +376,7 @@ void paged_decode_kernel(DecodeArgs a) {
             *reinterpret_cast<floatx4 *>(dst + 4) =
                 floatx4{acc[h][4], acc[h][5], acc[h][6], acc[h][7]};
             if (lr == 0) {
-              a.ws_ml[pr * 2] = m_run[h];
+              a.ws_ml[pr * 2] = m_run[h] * c;  // base-2 units
               a.ws_ml[pr * 2 + 1] = l_tot[h];
             }
           }
@@ -428,7 +398,7 @@ void paged_decode_kernel(DecodeArgs a) {
     if (lane == 0) {
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        red_m[w][h] = m_run[h];
+        red_m[w][h] = m_run[h] * c;  // base-2 units
         red_l[w][h] = l_tot[h];
       }
     }
