@@ -86,8 +86,10 @@ __device__ inline uint32_t pack2(float a, float b) {
 }
 
 // 16-lane row reductions with DPP (every lane of the row gets the result).
-// quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E, row_ror:4 = 0x124,
-// row_ror:8 = 0x128.
+// Each step pairs lanes symmetrically -- quad_perm [1,0,3,2] (0xB1) and
+// [2,3,0,1] (0x4E), row_half_mirror (0x141), row_mirror (0x140) -- so both
+// partners add the same two values and all 16 lanes end bit-identical
+// (rotations would pair lanes asymmetrically and let the rounding differ).
 template <int CTRL>
 __device__ inline float dpp_f(float v) {
   return __builtin_bit_cast(
@@ -98,16 +100,16 @@ __device__ inline float dpp_f(float v) {
 __device__ inline float row16_max(float v) {
   v = fmaxf(v, dpp_f<0xB1>(v));
   v = fmaxf(v, dpp_f<0x4E>(v));
-  v = fmaxf(v, dpp_f<0x124>(v));
-  v = fmaxf(v, dpp_f<0x128>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
   return v;
 }
 
 __device__ inline float row16_sum(float v) {
   v += dpp_f<0xB1>(v);
   v += dpp_f<0x4E>(v);
-  v += dpp_f<0x124>(v);
-  v += dpp_f<0x128>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
   return v;
 }
 
