@@ -130,4 +130,15 @@ __device__ inline float wave_max(float v) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Workgroup barrier that orders LDS accesses only.  The fences are scoped to
+// the local (LDS) address space, so the wait before s_barrier covers this
+// wave's LDS operations (lgkmcnt) while global loads issued earlier stay in
+// flight; __syncthreads() also waits for those (vmcnt(0)), which drains any
+// register prefetch at every barrier.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 }  // namespace mce

@@ -22,25 +22,49 @@
 // S^T output layout) is mirrored by the V^T reads, two 8-byte LDS reads of 4
 // consecutive keys each.  V is transposed into LDS ([dim][key]) on the way in;
 // K is stored row-major with a 16-byte row pad (conflict-free 16-byte reads).
-// The next tile's K/V are loaded into registers while the current tile is
-// computed.
 //
-// Softmax: p = exp2(s c - m c) with c = scale log2(e) as one FMA on the raw
-// score; only tiles that reach a wave's diagonal (or the sequence end) are
-// masked; the running max is only raised (and O, l rescaled) when a row's
-// max grows by more than 2^8 in p units, so most tiles skip the rescale
-// (p then stays below 256, well inside fp16).
+// Software pipeline: the scores of key tile k+1 are computed in the same
+// straight-line block as the softmax and P V of tile k, so the exp/convert
+// VALU work of one tile runs while the matrix cores work on the other.  K and
+// V^T are double-buffered in LDS (K one tile ahead of V) with one barrier per
+// tile; the next tiles are fetched into registers a full tile ahead.
+//
+// Softmax in the log2 domain: Q is pre-scaled by c = scale log2(e) when it is
+// loaded, and each score accumulator starts at -m (the row's running max, in
+// the same units), so the MFMA output is already the exp2 argument.  The
+// running max is only raised (O, l and the pending scores shifted) when a
+// row's max grows by more than 2^8 in p units, so most tiles skip it and p
+// stays below 256, well inside fp16.  Row sums are taken with v_dot2 over the
+// same f16 P values that enter P V.
 #include "mce_common.h"
 
 namespace mce {
 
 constexpr int PF_HD = 128;
-constexpr int PF_BN = 64;
+constexpr int PF_BN = 32;
 constexpr int KS_PITCH = PF_HD + 8;  // halfs per K row in LDS (272 B)
-constexpr int VT_PITCH = PF_BN + 4;  // halfs per V^T row in LDS (136 B)
+constexpr int VT_PITCH = PF_BN + 4;  // halfs per V^T row in LDS (72 B)
 constexpr float RESCALE_TAU = 8.0f;  // log2 headroom before raising the max
+// Buffer descriptor word 3 for raw (stride 0) dword loads on gfx9-family
+// parts: data format 32, no swizzle, range-checked against num_records.
+constexpr int BUF_RSRC_WORD3 = 0x00020000;
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+// max(x[l], x[l ^ 32]) in every lane: v_permlane32_swap exchanges the two
+// 32-lane halves, leaving each lane with both values of its pair.
+__device__ __forceinline__ float xor32_max(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+
+#ifndef PF_SCHEDULE
+#define PF_SCHEDULE()
+#endif
+#ifndef PF_WAVES_PER_EU
+#define PF_WAVES_PER_EU 2
+#endif
 
 struct PrefillArgs {
   const uint16_t *q, *k, *v;
@@ -51,16 +75,17 @@ struct PrefillArgs {
 };
 
 template <int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(PF_WAVES_PER_EU, PF_WAVES_PER_EU)))
 void prefill_causal_kernel(PrefillArgs a) {
   constexpr int BM = 32 * NW;
   constexpr int NT = NW * 64;
   constexpr int K_PIECES = PF_BN * PF_HD / 8;      // 16-byte pieces per K tile
-  constexpr int V_GROUPS = PF_BN / 4 * PF_HD / 8;  // 4-key x 8-dim groups per V tile
+  constexpr int V_GROUPS = PF_BN / 2 * PF_HD / 8;  // 2-key x 8-dim groups per V tile
   constexpr int KP = (K_PIECES + NT - 1) / NT;
   constexpr int VG = (V_GROUPS + NT - 1) / NT;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[PF_BN * KS_PITCH];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[PF_HD * VT_PITCH];
+  constexpr int KS_SIZE = PF_BN * KS_PITCH, VT_SIZE = PF_HD * VT_PITCH;
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * KS_SIZE];
+  __shared__ __attribute__((aligned(16))) uint16_t Vt[2 * VT_SIZE];
 
   // workgroup -> (item, batch, kv head); kv head fastest so that the
   // workgroups of one kv head share an XCD (and its L2) when Hkv B == 8.
@@ -82,217 +107,251 @@ void prefill_causal_kernel(PrefillArgs a) {
 
   // Per-thread staging assignments (fixed for the whole kernel).
   //  K: piece pc -> key pc / 16, 16-byte column pc % 16 (16 lanes per key row).
-  //  V: group gc -> keys 4 (gc % 16) .. +3, dims 8 (gc / 16) .. +7, so the 16
-  //     lanes of a group write one 128-byte run of a V^T row (no bank
-  //     conflicts) after transposing 4 keys x 8 dims in registers.
-  //  (NT is a multiple of 16, so piece it of this thread sits NT / 16 keys
-  //  below piece it - 1: one base offset plus a uniform step.)
-  static_assert(NT % 16 == 0, "staging assumes whole 16-lane groups");
-  const int k_off0 = (tid >> 4) * kv_row + (tid & 15) * 8;
-  const int k_step = (NT / 16) * kv_row;
-  int v_off[VG];
+  //  V: group gc -> keys 2 (gc % 16) .. +1, dims 8 (gc / 16) .. +7, so 16
+  //     lanes write one 64-byte run of a V^T row, the four runs of a wave
+  //     quarter landing 16 banks apart (no bank conflicts), after
+  //     transposing 2 keys x 8 dims in registers.
+  // Two register sets: a tile is fetched two iterations before it is staged.
+  // Loads are unconditional buffer loads (straight-line code keeps the
+  // compiler's vmcnt accounting exact, so staging waits only for the set it
+  // stores) with loop-invariant per-thread offsets; the hardware range check
+  // of the buffer descriptor returns zeros for keys at or past the sequence
+  // end (the descriptor spans this (batch, kv head)'s rows up to key S).
+  static_assert(KP * NT == K_PIECES && VG * NT == V_GROUPS, "whole tiles per thread");
+  const int kv_bytes = (S * kv_row - g * PF_HD) * 2;
+  const __amdgpu_buffer_rsrc_t krsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void *)kbase, (short)0, kv_bytes, BUF_RSRC_WORD3);
+  const __amdgpu_buffer_rsrc_t vrsrc =
+      __builtin_amdgcn_make_buffer_rsrc((void *)vbase, (short)0, kv_bytes, BUF_RSRC_WORD3);
+  int k_voff[KP], v_voff[VG * 2];
 #pragma unroll
-  for (int gi = 0; gi < VG; ++gi) {
-    const int gc = tid + gi * NT;
-    v_off[gi] = 4 * (gc & 15) * kv_row + (gc >> 4) * 8;
+  for (int it = 0; it < KP; ++it) {
+    const int pc = tid + it * NT;
+    k_voff[it] = ((pc >> 4) * kv_row + (pc & 15) * 8) * 2;
   }
-
-  u32x4 kreg[KP], vreg[VG * 4];
-  auto load_tile = [&](int n0) {
-    const uint16_t *kt = kbase + (int64_t)n0 * kv_row;
-    const uint16_t *vt = vbase + (int64_t)n0 * kv_row;
+#pragma unroll
+  for (int gi = 0; gi < VG; ++gi)
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int gc = tid + gi * NT;
+      v_voff[gi * 2 + kk] = ((2 * (gc & 15) + kk) * kv_row + (gc >> 4) * 8) * 2;
+    }
+  u32x4 kreg[2][KP], vreg[2][VG * 2];
+  auto load_k = [&](int set, int n0) {
+    const int tile_off = n0 * kv_row * 2;
+#pragma unroll
+    for (int it = 0; it < KP; ++it)
+      kreg[set][it] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krsrc, k_voff[it] + tile_off, 0, 0));
+  };
+  auto load_v = [&](int set, int n0) {
+    const int tile_off = n0 * kv_row * 2;
+#pragma unroll
+    for (int j = 0; j < VG * 2; ++j)
+      vreg[set][j] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrsrc, v_voff[j] + tile_off, 0, 0));
+  };
+  auto store_k = [&](int set, uint16_t *ks) {
 #pragma unroll
     for (int it = 0; it < KP; ++it) {
       const int pc = tid + it * NT;
-      const int key = n0 + (pc >> 4);
-      kreg[it] = (pc < K_PIECES && key < S)
-                     ? *reinterpret_cast<const u32x4 *>(kt + k_off0 + it * k_step)
-                     : u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int gi = 0; gi < VG; ++gi) {
-      const int gc = tid + gi * NT;
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int key = n0 + 4 * (gc & 15) + kk;
-        vreg[gi * 4 + kk] = (gc < V_GROUPS && key < S)
-                                ? *reinterpret_cast<const u32x4 *>(vt + v_off[gi] + kk * kv_row)
-                                : u32x4{0, 0, 0, 0};
-      }
+      *reinterpret_cast<u32x4 *>(&ks[(pc >> 4) * KS_PITCH + (pc & 15) * 8]) = kreg[set][it];
     }
   };
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int it = 0; it < KP; ++it) {
-      const int pc = tid + it * NT;
-      if (pc < K_PIECES)
-        *reinterpret_cast<u32x4 *>(&Ks[(pc >> 4) * KS_PITCH + (pc & 15) * 8]) = kreg[it];
-    }
+  auto store_v = [&](int set, uint16_t *vt) {
 #pragma unroll
     for (int gi = 0; gi < VG; ++gi) {
       const int gc = tid + gi * NT;
-      if (gc < V_GROUPS) {
-        const int key0 = 4 * (gc & 15), piece = gc >> 4;
-        const u32x4 *x = &vreg[gi * 4];
+      const int key0 = 2 * (gc & 15), piece = gc >> 4;
+      const u32x4 *x = &vreg[set][gi * 2];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // dims 8 piece + 2e (low halves) and + 2e + 1 (high halves)
-          u32x2 lo, hi;
-          lo[0] = __builtin_amdgcn_perm(x[1][e], x[0][e], 0x05040100u);
-          lo[1] = __builtin_amdgcn_perm(x[3][e], x[2][e], 0x05040100u);
-          hi[0] = __builtin_amdgcn_perm(x[1][e], x[0][e], 0x07060302u);
-          hi[1] = __builtin_amdgcn_perm(x[3][e], x[2][e], 0x07060302u);
-          const int d = piece * 8 + 2 * e;
-          *reinterpret_cast<u32x2 *>(&Vt[d * VT_PITCH + key0]) = lo;
-          *reinterpret_cast<u32x2 *>(&Vt[(d + 1) * VT_PITCH + key0]) = hi;
-        }
+      for (int e = 0; e < 4; ++e) {
+        // dims 8 piece + 2e (low halves) and + 2e + 1 (high halves)
+        const int d = piece * 8 + 2 * e;
+        *reinterpret_cast<uint32_t *>(&vt[d * VT_PITCH + key0]) =
+            __builtin_amdgcn_perm(x[1][e], x[0][e], 0x05040100u);
+        *reinterpret_cast<uint32_t *>(&vt[(d + 1) * VT_PITCH + key0]) =
+            __builtin_amdgcn_perm(x[1][e], x[0][e], 0x07060302u);
       }
     }
   };
 
   const int rows_total = S * G;
+  const int item = a.n_items - 1 - item_rank;  // heaviest items first
+  const int r_item = item * BM;
+  const int r_wave = r_item + 32 * w;
+  const int row = r_wave + r32;                 // this lane's row
+  const int pos = row / G, h = g * G + (row - pos * G);
+  const bool row_ok = row < rows_total;
+  const int wave_min_pos = r_wave / G;
+  const int item_max_pos = min(S - 1, (r_item + BM - 1) / G);
+  const int n_ktiles = item_max_pos / PF_BN + 1;  // tiles staged by the workgroup
+  // tiles this wave computes (none for a wave made only of padding rows)
+  const int n_wtiles =
+      r_wave < rows_total ? min(S - 1, min(r_wave + 31, rows_total - 1) / G) / PF_BN + 1 : 0;
+  // tiles [0, n_full) need no mask for this wave: every key <= its first
+  // position and < S
+  const int n_full = min((wave_min_pos + 1) / PF_BN, S / PF_BN);
+  const int lim = min(pos, S - 1) - 4 * hf;  // masked tiles: key offset limit + n0
+
+  // Q^T as MFMA B operand, pre-scaled by c: lane supplies
+  // c Q[pos, h][16 i + 8 hf + j].
+  half8 qreg[8];
   {
-    const int item = a.n_items - 1 - item_rank;  // heaviest items first
-    const int r_item = item * BM;
-    const int r_wave = r_item + 32 * w;
-    const int row = r_wave + r32;                 // this lane's row
-    const int pos = row / G, h = g * G + (row - pos * G);
-    const bool row_ok = row < rows_total;
-    const int wave_min_pos = r_wave / G;
-    const int wave_max_pos = min(S - 1, (r_wave + 31) / G);
-    const int item_max_pos = min(S - 1, (r_item + BM - 1) / G);
-    const int n_ktiles = item_max_pos / PF_BN + 1;
-    // tiles [0, n_full) need no mask for this wave: every key <= its first
-    // position and < S
-    const int n_full = min((wave_min_pos + 1) / PF_BN, S / PF_BN);
-    const int lim = min(pos, S - 1) - 4 * hf;  // masked tiles: key offset limit + n0
-
-    // Q^T as MFMA B operand: lane supplies Q[pos, h][16 i + 8 hf + j].
-    half8 qreg[8];
-    {
-      const uint16_t *qp = a.q + ((int64_t)b * S + (row_ok ? pos : 0)) * q_row_stride +
-                           (int64_t)(row_ok ? h : 0) * PF_HD + 8 * hf;
+    const uint16_t *qp = a.q + ((int64_t)b * S + (row_ok ? pos : 0)) * q_row_stride +
+                         (int64_t)(row_ok ? h : 0) * PF_HD + 8 * hf;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        qreg[i] = row_ok ? __builtin_bit_cast(
-                               half8, *reinterpret_cast<const u32x4 *>(qp + 16 * i))
-                         : half8{0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < 8; ++i) {
+      const half8 x = row_ok ? __builtin_bit_cast(
+                                   half8, *reinterpret_cast<const u32x4 *>(qp + 16 * i))
+                             : half8{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qreg[i][j] = (_Float16)((float)x[j] * c);
     }
+  }
 
-    float m_i = -INFINITY, l_i = 0.f;
-    floatx16 o[4];
+  // S^T of one 32-key tile, accumulators starting at `init`.
+  auto scores = [&](const uint16_t *ks, float init, floatx16 &st) {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int e = 0; e < 16; ++e) st[e] = init;
+    const uint16_t *kp = &ks[r32 * KS_PITCH + 8 * hf];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+    for (int i = 0; i < 8; ++i) {
+      half8 ka = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4 *>(kp + 16 * i));
+      st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[i], st, 0, 0, 0);
+    }
+  };
 
-    // One key tile: scores, (masked) online softmax, P V.
-    auto tile = [&](int n0, bool masked) {
-      floatx16 st[2];
+  float m_run = 0.f, l_i = 0.f;  // running max (scaled units), row-sum part
+  floatx16 o[4];
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh) {
+  for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) st[kh][e] = 0.f;
-        const uint16_t *kp = &Ks[(kh * 32 + r32) * KS_PITCH + 8 * hf];
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+  floatx16 s_a, s_b;  // scores of the current / next tile, ping-ponged
+  const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+
+  // Prologue: K_0 staged and scored; K_1 and V_0 staged into the second / first
+  // buffers; (K_2, V_1) fetched into register set 0 and (K_3, V_2) into set 1.
+  load_k(0, 0);
+  store_k(0, Ks);
+  load_k(0, PF_BN);
+  load_v(0, 0);
+  lds_barrier();
+  if (n_wtiles > 0) scores(Ks, 0.f, s_a);
+  store_k(0, Ks + KS_SIZE);
+  store_v(0, Vt);
+  load_k(0, 2 * PF_BN);
+  load_v(0, PF_BN);
+  load_k(1, 3 * PF_BN);
+  load_v(1, 2 * PF_BN);
+
+  // Iteration k: softmax + P V of tile k (scores already in s_cur), scores of
+  // tile k + 1 (K in buffer (k+1)%2), then stage K_{k+2} / V_{k+1} from
+  // register set k%2 into the buffers that iteration k - 1 finished reading
+  // and fetch K_{k+4} / V_{k+3} into that set.  Barriers match by count:
+  // every wave runs the same (even) number of iterations.  Staging is
+  // unconditional, so the loop carries the register sets without copies (a
+  // copy of a pending load would wait for every load in flight); tiles past
+  // the end are zero-filled and written to buffers nobody reads again.
+  auto step = [&](const int kt, const int set, floatx16 &s_cur, floatx16 &s_nxt) {
+    lds_barrier();
+    if (kt < n_wtiles) {
+      if (kt >= n_full) {  // diagonal / end-of-sequence tile
+        const int l2 = lim - kt * PF_BN;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          half8 ka = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4 *>(kp + 16 * i));
-          st[kh] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[i], st[kh], 0, 0, 0);
-        }
-      }
-      if (masked) {
-        const int l2 = lim - n0;
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-          for (int e = 0; e < 16; ++e)
-            if (kh * 32 + 8 * (e >> 2) + (e & 3) > l2) st[kh][e] = -INFINITY;
+        for (int e = 0; e < 16; ++e)
+          if (8 * (e >> 2) + (e & 3) > l2) s_cur[e] = -INFINITY;
       }
       float mx = -INFINITY;
 #pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, st[kh][e]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-      // raise the running max only when p would exceed 2^TAU
-      const bool grow = (mx - m_i) * c > RESCALE_TAU;  // true on the first tile
-      if (__ballot(grow)) {
-        const float m_new = grow ? mx : m_i;
-        const float alpha = fast_exp2((m_i - m_new) * c);
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_cur[e]);
+      mx = fmaxf(mx, xor32_max(mx));
+      // raise the running max on the first tile, or when p would exceed 2^TAU
+      const bool grow = kt == 0 || mx > RESCALE_TAU;
+      if (__builtin_expect(__ballot(grow) != 0, 0)) {
+        const float d = grow ? mx : 0.f;
+        const float alpha = kt == 0 ? 0.f : fast_exp2(-d);
         l_i *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
           for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-        m_i = m_new;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s_cur[e] -= d;
+        m_run += d;
       }
-      const float neg_mc = m_i == -INFINITY ? 0.f : -m_i * c;
-      float psum = 0.f;
-      half8 pk[2][2];
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int e2 = 0; e2 < 8; ++e2) {
-          const float p0 = fast_exp2(__builtin_fmaf(st[kh][2 * e2], c, neg_mc));
-          const float p1 = fast_exp2(__builtin_fmaf(st[kh][2 * e2 + 1], c, neg_mc));
-          psum += p0 + p1;
-          const h2 pp = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(p0, p1));
-          pk[kh][e2 >> 2][2 * (e2 & 3)] = pp[0];
-          pk[kh][e2 >> 2][2 * (e2 & 3) + 1] = pp[1];
-        }
-      l_i += psum;
-      // O^T += V^T P^T
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const uint16_t *vp = &Vt[(dt * 32 + r32) * VT_PITCH + 4 * hf];
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) {
-            const int kb = kh * 32 + 16 * kk;
-            u32x2 x0 = *reinterpret_cast<const u32x2 *>(vp + kb);
-            u32x2 x1 = *reinterpret_cast<const u32x2 *>(vp + kb + 8);
-            u32x4 xa = {x0[0], x0[1], x1[0], x1[1]};
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                __builtin_bit_cast(half8, xa), pk[kh][kk], o[dt], 0, 0, 0);
-          }
-      }
-    };
 
-    // Barriers match by count, so the two loops may split at a different tile
-    // in each wave: every iteration of either loop stages exactly one tile.
-    load_tile(0);
-    int kt = 0;
-    for (; kt < n_full; ++kt) {  // tiles entirely below this wave's rows
-      __syncthreads();
-      store_tile();
-      __syncthreads();
-      if (kt + 1 < n_ktiles) load_tile((kt + 1) * PF_BN);
-      tile(kt * PF_BN, false);
-    }
-    for (; kt < n_ktiles; ++kt) {  // diagonal / end-of-sequence tiles
-      __syncthreads();
-      store_tile();
-      __syncthreads();
-      if (kt + 1 < n_ktiles) load_tile((kt + 1) * PF_BN);
-      if (kt * PF_BN <= wave_max_pos) tile(kt * PF_BN, true);
-    }
-
-    // ---- normalise and store: lane holds dims dt*32 + 8(e/4) + 4hf + e%4 ----
-    const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
-    if (row_ok) {
-      const float inv = 1.0f / l_tot;
-      uint16_t *op = a.out + ((int64_t)b * S + pos) * q_row_stride + (int64_t)h * PF_HD + 4 * hf;
+      // ---- one straight-line block: scores of tile k+1 || exp + P V of tile k.
+      // All LDS operands of the block are fetched first (K fragments of tile
+      // k+1, V^T fragments of tile k), so their latency overlaps the first
+      // MFMAs and the exp work instead of stalling each MFMA in turn.
+      const uint16_t *kp = &Ks[((kt + 1) & 1) * KS_SIZE + r32 * KS_PITCH + 8 * hf];
+      const uint16_t *vp = &Vt[(kt & 1) * VT_SIZE + r32 * VT_PITCH + 4 * hf];
+      half8 kf[8];
+      u32x4 vf[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        kf[i] = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4 *>(kp + 16 * i));
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {
-          u32x2 pr;
-          pr[0] = pack2<F16T>(o[dt][4 * e4] * inv, o[dt][4 * e4 + 1] * inv);
-          pr[1] = pack2<F16T>(o[dt][4 * e4 + 2] * inv, o[dt][4 * e4 + 3] * inv);
-          *reinterpret_cast<u32x2 *>(op + dt * 32 + 8 * e4) = pr;
+        for (int kk = 0; kk < 2; ++kk) {
+          const uint16_t *v = vp + dt * 32 * VT_PITCH + 16 * kk;
+          const u32x2 x0 = *reinterpret_cast<const u32x2 *>(v);
+          const u32x2 x1 = *reinterpret_cast<const u32x2 *>(v + 8);
+          vf[dt * 2 + kk] = u32x4{x0[0], x0[1], x1[0], x1[1]};
         }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s_nxt[e] = -m_run;
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i], qreg[i], s_nxt, 0, 0, 0);
+      half8 pk[2];
+#pragma unroll
+      for (int e2 = 0; e2 < 8; ++e2) {
+        const float p0 = fast_exp2(s_cur[2 * e2]);
+        const float p1 = fast_exp2(s_cur[2 * e2 + 1]);
+        const h2 pp = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(p0, p1));
+        l_i = __builtin_amdgcn_fdot2(pp, ones, l_i, false);
+        pk[e2 >> 2][2 * (e2 & 3)] = pp[0];
+        pk[e2 >> 2][2 * (e2 & 3) + 1] = pp[1];
+      }
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, vf[dt * 2 + kk]),
+                                                         pk[kk], o[dt], 0, 0, 0);
+      PF_SCHEDULE();
     }
+    // stage K_{k+2} into buffer k%2 (read as K_k in iteration k-1) and
+    // V_{k+1} into buffer (k+1)%2 (read as V_{k-1} in iteration k-1)
+    store_k(set, Ks + (kt & 1) * KS_SIZE);
+    store_v(set, Vt + ((kt + 1) & 1) * VT_SIZE);
+    load_k(set, (kt + 4) * PF_BN);
+    load_v(set, (kt + 3) * PF_BN);
+  };
+  for (int kt = 0; kt < n_ktiles; kt += 2) {
+    step(kt, 0, s_a, s_b);
+    step(kt + 1, 1, s_b, s_a);
+  }
+
+  // ---- normalise and store: lane holds dims dt*32 + 8(e/4) + 4hf + e%4 ----
+  const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
+  if (row_ok) {
+    const float inv = 1.0f / l_tot;
+    uint16_t *op = a.out + ((int64_t)b * S + pos) * q_row_stride + (int64_t)h * PF_HD + 4 * hf;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        u32x2 pr;
+        pr[0] = pack2<F16T>(o[dt][4 * e4] * inv, o[dt][4 * e4 + 1] * inv);
+        pr[1] = pack2<F16T>(o[dt][4 * e4 + 2] * inv, o[dt][4 * e4 + 3] * inv);
+        *reinterpret_cast<u32x2 *>(op + dt * 32 + 8 * e4) = pr;
+      }
   }
 }
 
@@ -325,6 +384,10 @@ extern "C" int mce_prefill_attention(int dtype, const void *query,
               "mce_prefill_attention: tensors must be 16-byte aligned");
   const int G = num_heads / num_kv_heads;
   MCE_REQUIRE((int64_t)seq_len * G < ((int64_t)1 << 30), "mce_prefill_attention: sequence too long");
+  // K/V tiles are addressed with 32-bit byte offsets within one batch entry
+  // (including the prefetch of up to 5 tiles past the end)
+  MCE_REQUIRE(((int64_t)seq_len + 256) * num_kv_heads * head_dim * 2 < ((int64_t)1 << 31),
+              "mce_prefill_attention: seq_len * num_kv_heads too large");
   // Items of 128 rows, one per workgroup, heaviest first: when there are more
   // items than workgroup slots, the dispatcher hands the lighter ones to the
   // CUs that free up first (longest-processing-time-first scheduling).
