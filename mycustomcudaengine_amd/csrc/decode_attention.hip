@@ -480,22 +480,6 @@ __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
   a.out[row * HD + d] = F16T::from_float(A / L);
 }
 
-// Workgroups per kv-head group: about one 8-wave workgroup per CU over the
-// whole grid, at most 512.
-static int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 struct DecodeLayout {
   int J, hpg, wph, groups;
   size_t ml_off, acc_off, nparts_off, total;

@@ -21,6 +21,9 @@ void clear_error();
 // Maps a failed launch (hipGetLastError after the launch) to MCE_ERR_LAUNCH.
 int check_launch(const char *what);
 
+// Compute units of the current device (cached per device; 256 if unknown).
+int cu_count();
+
 inline bool is_pow2(int64_t x) { return x > 0 && (x & (x - 1)) == 0; }
 inline int ilog2(int64_t x) {
   int r = 0;

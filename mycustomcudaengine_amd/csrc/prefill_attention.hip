@@ -19,8 +19,9 @@
 //     from the S^T registers, converted to f16): lane l again holds row
 //     (l % 32), so the online-softmax rescale is a per-lane multiply.
 // The k-index permutation used for P^T (keys 8(v/4) + 4(l/32) + v%4 of the
-// S^T output layout) is mirrored by the V^T reads, two 8-byte LDS reads of 4
-// consecutive keys each.  V is transposed into LDS ([dim][key]) on the way in;
+// S^T output layout) is mirrored by the V^T reads: V is transposed into LDS
+// ([dim][key], keys of each 16-key group stored in the order the fragments
+// consume them) on the way in, so every MFMA operand is one 16-byte LDS read;
 // K is stored row-major with a 16-byte row pad (conflict-free 16-byte reads).
 //
 // Software pipeline: the scores of key tile k+1 are computed in the same
@@ -43,7 +44,7 @@ namespace mce {
 constexpr int PF_HD = 128;
 constexpr int PF_BN = 32;
 constexpr int KS_PITCH = PF_HD + 8;  // halfs per K row in LDS (272 B)
-constexpr int VT_PITCH = PF_BN + 4;  // halfs per V^T row in LDS (72 B)
+constexpr int VT_PITCH = PF_BN + 8;  // halfs per V^T row in LDS (80 B)
 constexpr float RESCALE_TAU = 8.0f;  // log2 headroom before raising the max
 // Buffer descriptor word 3 for raw (stride 0) dword loads on gfx9-family
 // parts: data format 32, no swizzle, range-checked against num_records.
@@ -51,12 +52,28 @@ constexpr int BUF_RSRC_WORD3 = 0x00020000;
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
+// Position of key offset o (0..31) within a V^T row: bits 2 and 3 swapped,
+// so the 8 keys one lane feeds to a P V MFMA (4 hf + 0..3 and 8 + 4 hf + 0..3
+// of a 16-key group) sit in 16 contiguous bytes: one ds_read_b128 per
+// fragment.  The 80-byte row pitch keeps those reads conflict-free (16 rows
+// step through 16 distinct 4-bank groups).
+__device__ __forceinline__ int vt_pos(int o) {
+  return (o & ~12) | ((o & 4) << 1) | ((o & 8) >> 1);
+}
+
 // max(x[l], x[l ^ 32]) in every lane: v_permlane32_swap exchanges the two
 // 32-lane halves, leaving each lane with both values of its pair.
 __device__ __forceinline__ float xor32_max(float x) {
   const unsigned u = __builtin_bit_cast(unsigned, x);
   const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
   return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+
+// x[l] + x[l ^ 32] in every lane (the same sum in both lanes of a pair).
+__device__ __forceinline__ float xor32_add(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
 }
 
 #ifndef PF_SCHEDULE
@@ -74,18 +91,29 @@ struct PrefillArgs {
   float scale_log2;
 };
 
-template <int NW>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(PF_WAVES_PER_EU, PF_WAVES_PER_EU)))
+// NRB row blocks of 32 rows per workgroup and KSPLIT key streams: wave w owns
+// row block w % NRB and key stream kh = w / NRB, which takes key tiles kh,
+// kh + KSPLIT, kh + 2 KSPLIT, ...  With KSPLIT = 2 every SIMD runs two waves
+// of the same rows and the longest serial chain (the causal diagonal item) is
+// halved; the streams keep separate online-softmax states that are merged
+// through LDS at the end.  KSPLIT = 1 suits grids with several workgroups
+// per CU, where the co-resident workgroups already fill the SIMDs.
+template <int NRB, int KSPLIT>
+__global__ __launch_bounds__(NRB * KSPLIT * 64) __attribute__((amdgpu_waves_per_eu(PF_WAVES_PER_EU, PF_WAVES_PER_EU)))
 void prefill_causal_kernel(PrefillArgs a) {
-  constexpr int BM = 32 * NW;
-  constexpr int NT = NW * 64;
+  constexpr int BM = 32 * NRB;
+  constexpr int NT = NRB * 64;                     // threads per key stream
   constexpr int K_PIECES = PF_BN * PF_HD / 8;      // 16-byte pieces per K tile
   constexpr int V_GROUPS = PF_BN / 2 * PF_HD / 8;  // 2-key x 8-dim groups per V tile
-  constexpr int KP = (K_PIECES + NT - 1) / NT;
-  constexpr int VG = (V_GROUPS + NT - 1) / NT;
+  constexpr int KP = K_PIECES / NT;
+  constexpr int VG = V_GROUPS / NT;
+  static_assert(KP * NT == K_PIECES && VG * NT == V_GROUPS, "whole tiles per thread");
   constexpr int KS_SIZE = PF_BN * KS_PITCH, VT_SIZE = PF_HD * VT_PITCH;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2 * KS_SIZE];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2 * VT_SIZE];
+  // [key stream][double buffer] K and V^T tiles; reused for the final merge
+  constexpr int LDS_HALFS = 2 * KSPLIT * (KS_SIZE + VT_SIZE);
+  __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALFS];
+  uint16_t *const Ks = lds;
+  uint16_t *const Vt = lds + 2 * KSPLIT * KS_SIZE;
 
   // workgroup -> (item, batch, kv head); kv head fastest so that the
   // workgroups of one kv head share an XCD (and its L2) when Hkv B == 8.
@@ -97,7 +125,11 @@ void prefill_causal_kernel(PrefillArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rb = w % NRB, kh = w / NRB;
+  const int tid_h = tid - kh * NT;  // thread index within the key stream
   const int hf = lane >> 5, r32 = lane & 31;
+  uint16_t *const ks_h = Ks + kh * 2 * KS_SIZE;
+  uint16_t *const vt_h = Vt + kh * 2 * VT_SIZE;
 
   const int64_t q_row_stride = (int64_t)a.Hq * PF_HD;
   const int kv_row = a.Hkv * PF_HD;  // elements between consecutive keys
@@ -105,19 +137,16 @@ void prefill_causal_kernel(PrefillArgs a) {
   const uint16_t *vbase = a.v + ((int64_t)b * S * a.Hkv + g) * PF_HD;
   const float c = a.scale_log2;
 
-  // Per-thread staging assignments (fixed for the whole kernel).
+  // Per-thread staging assignments within a key stream (fixed for the kernel).
   //  K: piece pc -> key pc / 16, 16-byte column pc % 16 (16 lanes per key row).
-  //  V: group gc -> keys 2 (gc % 16) .. +1, dims 8 (gc / 16) .. +7, so 16
-  //     lanes write one 64-byte run of a V^T row, the four runs of a wave
-  //     quarter landing 16 banks apart (no bank conflicts), after
-  //     transposing 2 keys x 8 dims in registers.
+  //  V: group gc -> keys 2 (gc % 16) .. +1, dims 8 (gc / 16) .. +7: after a
+  //     2-key x 8-dim transpose in registers, 16 lanes write one V^T row run.
   // Two register sets: a tile is fetched two iterations before it is staged.
   // Loads are unconditional buffer loads (straight-line code keeps the
   // compiler's vmcnt accounting exact, so staging waits only for the set it
   // stores) with loop-invariant per-thread offsets; the hardware range check
   // of the buffer descriptor returns zeros for keys at or past the sequence
   // end (the descriptor spans this (batch, kv head)'s rows up to key S).
-  static_assert(KP * NT == K_PIECES && VG * NT == V_GROUPS, "whole tiles per thread");
   const int kv_bytes = (S * kv_row - g * PF_HD) * 2;
   const __amdgpu_buffer_rsrc_t krsrc =
       __builtin_amdgcn_make_buffer_rsrc((void *)kbase, (short)0, kv_bytes, BUF_RSRC_WORD3);
@@ -126,51 +155,53 @@ void prefill_causal_kernel(PrefillArgs a) {
   int k_voff[KP], v_voff[VG * 2];
 #pragma unroll
   for (int it = 0; it < KP; ++it) {
-    const int pc = tid + it * NT;
+    const int pc = tid_h + it * NT;
     k_voff[it] = ((pc >> 4) * kv_row + (pc & 15) * 8) * 2;
   }
 #pragma unroll
   for (int gi = 0; gi < VG; ++gi)
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const int gc = tid + gi * NT;
+      const int gc = tid_h + gi * NT;
       v_voff[gi * 2 + kk] = ((2 * (gc & 15) + kk) * kv_row + (gc >> 4) * 8) * 2;
     }
+  // stream index u of this key stream <-> key tile KSPLIT u + kh
+  auto tile_off = [&](int u) { return (KSPLIT * u + kh) * PF_BN * kv_row * 2; };
   u32x4 kreg[2][KP], vreg[2][VG * 2];
-  auto load_k = [&](int set, int n0) {
-    const int tile_off = n0 * kv_row * 2;
+  auto load_k = [&](int set, int u) {
+    const int off = tile_off(u);
 #pragma unroll
     for (int it = 0; it < KP; ++it)
       kreg[set][it] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krsrc, k_voff[it] + tile_off, 0, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krsrc, k_voff[it] + off, 0, 0));
   };
-  auto load_v = [&](int set, int n0) {
-    const int tile_off = n0 * kv_row * 2;
+  auto load_v = [&](int set, int u) {
+    const int off = tile_off(u);
 #pragma unroll
     for (int j = 0; j < VG * 2; ++j)
       vreg[set][j] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrsrc, v_voff[j] + tile_off, 0, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrsrc, v_voff[j] + off, 0, 0));
   };
   auto store_k = [&](int set, uint16_t *ks) {
 #pragma unroll
     for (int it = 0; it < KP; ++it) {
-      const int pc = tid + it * NT;
+      const int pc = tid_h + it * NT;
       *reinterpret_cast<u32x4 *>(&ks[(pc >> 4) * KS_PITCH + (pc & 15) * 8]) = kreg[set][it];
     }
   };
   auto store_v = [&](int set, uint16_t *vt) {
 #pragma unroll
     for (int gi = 0; gi < VG; ++gi) {
-      const int gc = tid + gi * NT;
+      const int gc = tid_h + gi * NT;
       const int key0 = 2 * (gc & 15), piece = gc >> 4;
       const u32x4 *x = &vreg[set][gi * 2];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         // dims 8 piece + 2e (low halves) and + 2e + 1 (high halves)
         const int d = piece * 8 + 2 * e;
-        *reinterpret_cast<uint32_t *>(&vt[d * VT_PITCH + key0]) =
+        *reinterpret_cast<uint32_t *>(&vt[d * VT_PITCH + vt_pos(key0)]) =
             __builtin_amdgcn_perm(x[1][e], x[0][e], 0x05040100u);
-        *reinterpret_cast<uint32_t *>(&vt[(d + 1) * VT_PITCH + key0]) =
+        *reinterpret_cast<uint32_t *>(&vt[(d + 1) * VT_PITCH + vt_pos(key0)]) =
             __builtin_amdgcn_perm(x[1][e], x[0][e], 0x07060302u);
       }
     }
@@ -179,14 +210,16 @@ void prefill_causal_kernel(PrefillArgs a) {
   const int rows_total = S * G;
   const int item = a.n_items - 1 - item_rank;  // heaviest items first
   const int r_item = item * BM;
-  const int r_wave = r_item + 32 * w;
+  const int r_wave = r_item + 32 * rb;
   const int row = r_wave + r32;                 // this lane's row
   const int pos = row / G, h = g * G + (row - pos * G);
   const bool row_ok = row < rows_total;
   const int wave_min_pos = r_wave / G;
   const int item_max_pos = min(S - 1, (r_item + BM - 1) / G);
-  const int n_ktiles = item_max_pos / PF_BN + 1;  // tiles staged by the workgroup
-  // tiles this wave computes (none for a wave made only of padding rows)
+  const int n_ktiles = item_max_pos / PF_BN + 1;  // key tiles of the item
+  // iterations per key stream, rounded up to even for the ping-pong unroll
+  const int n_iter = ((n_ktiles + KSPLIT - 1) / KSPLIT + 1) / 2 * 2;
+  // key tiles this wave's rows need (none for a block of padding rows)
   const int n_wtiles =
       r_wave < rows_total ? min(S - 1, min(r_wave + 31, rows_total - 1) / G) / PF_BN + 1 : 0;
   // tiles [0, n_full) need no mask for this wave: every key <= its first
@@ -222,7 +255,10 @@ void prefill_causal_kernel(PrefillArgs a) {
     }
   };
 
-  float m_run = 0.f, l_i = 0.f;  // running max (scaled units), row-sum part
+  // Running max m_run (scaled units) is 0 until the row has seen an unmasked
+  // key (m_set); l_i is this lane's half of the row sum.
+  float m_run = 0.f, l_i = 0.f;
+  bool m_set = false;
   floatx16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
@@ -231,31 +267,33 @@ void prefill_causal_kernel(PrefillArgs a) {
   floatx16 s_a, s_b;  // scores of the current / next tile, ping-ponged
   const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
 
-  // Prologue: K_0 staged and scored; K_1 and V_0 staged into the second / first
-  // buffers; (K_2, V_1) fetched into register set 0 and (K_3, V_2) into set 1.
+  // Prologue (per key stream): K_0 staged and scored; K_1 and V_0 staged into
+  // the second / first buffers; (K_2, V_1) fetched into register set 0 and
+  // (K_3, V_2) into set 1 (indices are stream indices u).
   load_k(0, 0);
-  store_k(0, Ks);
-  load_k(0, PF_BN);
+  store_k(0, ks_h);
+  load_k(0, 1);
   load_v(0, 0);
   lds_barrier();
-  if (n_wtiles > 0) scores(Ks, 0.f, s_a);
-  store_k(0, Ks + KS_SIZE);
-  store_v(0, Vt);
-  load_k(0, 2 * PF_BN);
-  load_v(0, PF_BN);
-  load_k(1, 3 * PF_BN);
-  load_v(1, 2 * PF_BN);
+  if (kh < n_wtiles) scores(ks_h, 0.f, s_a);
+  store_k(0, ks_h + KS_SIZE);
+  store_v(0, vt_h);
+  load_k(0, 2);
+  load_v(0, 1);
+  load_k(1, 3);
+  load_v(1, 2);
 
-  // Iteration k: softmax + P V of tile k (scores already in s_cur), scores of
-  // tile k + 1 (K in buffer (k+1)%2), then stage K_{k+2} / V_{k+1} from
-  // register set k%2 into the buffers that iteration k - 1 finished reading
-  // and fetch K_{k+4} / V_{k+3} into that set.  Barriers match by count:
+  // Iteration u: softmax + P V of tile u (scores already in s_cur), scores of
+  // tile u + 1 (K in buffer (u+1)%2), then stage K_{u+2} / V_{u+1} from
+  // register set u%2 into the buffers that iteration u - 1 finished reading
+  // and fetch K_{u+4} / V_{u+3} into that set.  Barriers match by count:
   // every wave runs the same (even) number of iterations.  Staging is
   // unconditional, so the loop carries the register sets without copies (a
   // copy of a pending load would wait for every load in flight); tiles past
   // the end are zero-filled and written to buffers nobody reads again.
-  auto step = [&](const int kt, const int set, floatx16 &s_cur, floatx16 &s_nxt) {
+  auto step = [&](const int u, const int set, floatx16 &s_cur, floatx16 &s_nxt) {
     lds_barrier();
+    const int kt = KSPLIT * u + kh;  // key tile
     if (kt < n_wtiles) {
       if (kt >= n_full) {  // diagonal / end-of-sequence tile
         const int l2 = lim - kt * PF_BN;
@@ -267,11 +305,12 @@ void prefill_causal_kernel(PrefillArgs a) {
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_cur[e]);
       mx = fmaxf(mx, xor32_max(mx));
-      // raise the running max on the first tile, or when p would exceed 2^TAU
-      const bool grow = kt == 0 || mx > RESCALE_TAU;
+      // set the running max at the row's first unmasked key, raise it when p
+      // would exceed 2^TAU
+      const bool grow = m_set ? mx > RESCALE_TAU : mx > -INFINITY;
       if (__builtin_expect(__ballot(grow) != 0, 0)) {
         const float d = grow ? mx : 0.f;
-        const float alpha = kt == 0 ? 0.f : fast_exp2(-d);
+        const float alpha = m_set ? fast_exp2(-d) : 0.f;
         l_i *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
@@ -280,14 +319,15 @@ void prefill_causal_kernel(PrefillArgs a) {
 #pragma unroll
         for (int e = 0; e < 16; ++e) s_cur[e] -= d;
         m_run += d;
+        m_set = m_set || grow;
       }
 
-      // ---- one straight-line block: scores of tile k+1 || exp + P V of tile k.
+      // ---- one straight-line block: scores of tile u+1 || exp + P V of tile u.
       // All LDS operands of the block are fetched first (K fragments of tile
-      // k+1, V^T fragments of tile k), so their latency overlaps the first
+      // u+1, V^T fragments of tile u), so their latency overlaps the first
       // MFMAs and the exp work instead of stalling each MFMA in turn.
-      const uint16_t *kp = &Ks[((kt + 1) & 1) * KS_SIZE + r32 * KS_PITCH + 8 * hf];
-      const uint16_t *vp = &Vt[(kt & 1) * VT_SIZE + r32 * VT_PITCH + 4 * hf];
+      const uint16_t *kp = &ks_h[((u + 1) & 1) * KS_SIZE + r32 * KS_PITCH + 8 * hf];
+      const uint16_t *vp = &vt_h[(u & 1) * VT_SIZE + r32 * VT_PITCH + 8 * hf];
       half8 kf[8];
       u32x4 vf[8];
 #pragma unroll
@@ -296,12 +336,9 @@ void prefill_causal_kernel(PrefillArgs a) {
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const uint16_t *v = vp + dt * 32 * VT_PITCH + 16 * kk;
-          const u32x2 x0 = *reinterpret_cast<const u32x2 *>(v);
-          const u32x2 x1 = *reinterpret_cast<const u32x2 *>(v + 8);
-          vf[dt * 2 + kk] = u32x4{x0[0], x0[1], x1[0], x1[1]};
-        }
+        for (int kk = 0; kk < 2; ++kk)
+          vf[dt * 2 + kk] =
+              *reinterpret_cast<const u32x4 *>(vp + dt * 32 * VT_PITCH + 16 * kk);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int e = 0; e < 16; ++e) s_nxt[e] = -m_run;
@@ -326,30 +363,70 @@ void prefill_causal_kernel(PrefillArgs a) {
                                                          pk[kk], o[dt], 0, 0, 0);
       PF_SCHEDULE();
     }
-    // stage K_{k+2} into buffer k%2 (read as K_k in iteration k-1) and
-    // V_{k+1} into buffer (k+1)%2 (read as V_{k-1} in iteration k-1)
-    store_k(set, Ks + (kt & 1) * KS_SIZE);
-    store_v(set, Vt + ((kt + 1) & 1) * VT_SIZE);
-    load_k(set, (kt + 4) * PF_BN);
-    load_v(set, (kt + 3) * PF_BN);
+    // stage K_{u+2} into buffer u%2 (read as K_u in iteration u-1) and
+    // V_{u+1} into buffer (u+1)%2 (read as V_{u-1} in iteration u-1)
+    store_k(set, ks_h + (u & 1) * KS_SIZE);
+    store_v(set, vt_h + ((u + 1) & 1) * VT_SIZE);
+    load_k(set, u + 4);
+    load_v(set, u + 3);
   };
-  for (int kt = 0; kt < n_ktiles; kt += 2) {
-    step(kt, 0, s_a, s_b);
-    step(kt + 1, 1, s_b, s_a);
+  for (int u = 0; u < n_iter; u += 2) {
+    step(u, 0, s_a, s_b);
+    step(u + 1, 1, s_b, s_a);
   }
 
-  // ---- normalise and store: lane holds dims dt*32 + 8(e/4) + 4hf + e%4 ----
-  const float l_tot = l_i + __shfl_xor(l_i, 32, 64);
+  // ---- merge the key streams through LDS (KSPLIT = 2), normalise, store.
+  // Stream 1 publishes (m, l, O) per lane; stream 0 rescales both states to
+  // the larger max, adds them and writes the rows.  O^T is exchanged
+  // register-major (64 lanes x 4 bytes contiguous per register).
+  float m0 = m_set ? m_run : -INFINITY, a0 = 1.f, l_own = l_i;
+  const float *xo = nullptr;
+  float a1 = 0.f;
+  if constexpr (KSPLIT == 2) {
+    float *xo_w = reinterpret_cast<float *>(lds);  // [NRB][64 registers][64 lanes]
+    float *xm = xo_w + NRB * 64 * 64;              // [NRB][2][64 lanes]
+    static_assert((NRB * 64 * 64 + NRB * 2 * 64) * 4 <= LDS_HALFS * 2,
+                  "merge buffers fit in the staging LDS");
+    lds_barrier();  // every wave is done with the K / V^T tiles
+    if (kh == 1) {
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xo_w[(rb * 64 + dt * 16 + e) * 64 + lane] = o[dt][e];
+      xm[(rb * 2 + 0) * 64 + lane] = m0;
+      xm[(rb * 2 + 1) * 64 + lane] = l_i;
+    }
+    lds_barrier();
+    if (kh == 1) return;
+    // a state that never saw an unmasked key (m = -inf, l = 0, O = 0) gets
+    // weight 0
+    const float m1 = xm[(rb * 2 + 0) * 64 + lane];
+    const float l1 = xm[(rb * 2 + 1) * 64 + lane];
+    const float mm = fmaxf(m0, m1);
+    a0 = fast_exp2(m0 - mm);
+    a1 = fast_exp2(m1 - mm);
+    l_own = l_i * a0 + l1 * a1;
+    xo = xo_w + rb * 64 * 64 + lane;
+  }
+  const float l_tot = xor32_add(l_own);
   if (row_ok) {
     const float inv = 1.0f / l_tot;
+    const float s0 = a0 * inv, s1 = a1 * inv;
     uint16_t *op = a.out + ((int64_t)b * S + pos) * q_row_stride + (int64_t)h * PF_HD + 4 * hf;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int e4 = 0; e4 < 4; ++e4) {
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int e = 4 * e4 + j;
+          v[j] = o[dt][e] * s0;
+          if constexpr (KSPLIT == 2) v[j] += xo[(dt * 16 + e) * 64] * s1;
+        }
         u32x2 pr;
-        pr[0] = pack2<F16T>(o[dt][4 * e4] * inv, o[dt][4 * e4 + 1] * inv);
-        pr[1] = pack2<F16T>(o[dt][4 * e4 + 2] * inv, o[dt][4 * e4 + 3] * inv);
+        pr[0] = pack2<F16T>(v[0], v[1]);
+        pr[1] = pack2<F16T>(v[2], v[3]);
         *reinterpret_cast<u32x2 *>(op + dt * 32 + 8 * e4) = pr;
       }
   }
@@ -391,7 +468,9 @@ extern "C" int mce_prefill_attention(int dtype, const void *query,
   // Items of 128 rows, one per workgroup, heaviest first: when there are more
   // items than workgroup slots, the dispatcher hands the lighter ones to the
   // CUs that free up first (longest-processing-time-first scheduling).
-  constexpr int nw = 4;
+  constexpr int nrb = 4;
+  // Split the key range over two wave sets when the grid alone would not
+  // give every CU about two workgroups (long causal sequences, small batch).
   PrefillArgs a{};
   a.q = (const uint16_t *)query;
   a.k = (const uint16_t *)key;
@@ -402,11 +481,14 @@ extern "C" int mce_prefill_attention(int dtype, const void *query,
   a.Hq = num_heads;
   a.Hkv = num_kv_heads;
   a.G = G;
-  a.n_items = (int)(((int64_t)seq_len * G + 32 * nw - 1) / (32 * nw));
+  a.n_items = (int)(((int64_t)seq_len * G + 32 * nrb - 1) / (32 * nrb));
   a.scale_log2 = scale * 1.4426950408889634f;
   const int64_t grid = (int64_t)a.n_items * batch * num_kv_heads;
   MCE_REQUIRE(grid < ((int64_t)1 << 31), "mce_prefill_attention: problem too large");
   hipStream_t st = (hipStream_t)stream;
-  prefill_causal_kernel<nw><<<(unsigned)grid, nw * 64, 0, st>>>(a);
+  if (grid < 2 * (int64_t)cu_count())
+    prefill_causal_kernel<nrb, 2><<<(unsigned)grid, nrb * 128, 0, st>>>(a);
+  else
+    prefill_causal_kernel<nrb, 1><<<(unsigned)grid, nrb * 64, 0, st>>>(a);
   return check_launch("mce_prefill_attention");
 }

@@ -176,9 +176,22 @@ def test_prefill_matches_oracle(dev, s, hq, hkv):
     assert err <= TOL, err
 
 
+@pytest.mark.parametrize("b,s", [(8, 512), (6, 700)])
+def test_prefill_large_grid_matches_oracle(dev, b, s):
+    """Grids of at least two workgroups per CU take the kernel without the
+    in-workgroup key split (the small cases above take the split one)."""
+    case = make_prefill_case(60 + s, b, s)
+    out = ops.prefill_attention(case.query.to(dev), case.key.to(dev), case.value.to(dev),
+                                case.scale).cpu()
+    ref = prefill_attention_ref(case.query, case.key, case.value, case.scale)
+    assert not torch.isnan(out).any()
+    err = (out.float() - ref).abs().max().item()
+    assert err <= TOL, err
+
+
 def test_prefill_first_row_is_v0(dev):
-    """Row 0 attends to key 0 only, so its output is v_0 up to one rounding of
-    p = exp2(s c - m c) (computed as one FMA) and of the fp16 store."""
+    """Row 0 attends to key 0 only, so its output is v_0 up to the rounding of
+    p (exactly 1 when the running max is that score) and of the fp16 store."""
     case = make_prefill_case(30, 1, 200)
     out = ops.prefill_attention(case.query.to(dev), case.key.to(dev), case.value.to(dev),
                                 case.scale).cpu()
