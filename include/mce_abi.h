@@ -151,6 +151,28 @@ MCE_API int mce_rope_inplace(int dtype, void *query, void *key, const float *cos
                      int64_t k_stride_h, void *stream);
 
 /*
+ * RoPE of query and key in place, then the paged store of the rotated key and
+ * of value: the same result, bit for bit, as mce_rope_inplace (batch =
+ * num_tokens, seq_len = 1) followed by mce_paged_kv_store on the same tokens,
+ * in one launch.  With query_out non-null the rotated query goes to the
+ * contiguous rows query_out[num_tokens, num_heads, head_dim] instead (query
+ * untouched), ready for mce_paged_attention_decode.  Tokens are flat: positions[t] and slot_mapping[t] per
+ * token; query/key/value rows are addressed by (token, head) strides in
+ * elements.  No single counterpart in the reference: it fuses the two calls
+ * its decode step makes back to back (engine/models/llama.py:117-127 calls
+ * rope_inplace, then paged_kv_store), for the engine's decode and prefill.
+ */
+MCE_API int mce_rope_kv_store(int dtype, void *query, void *query_out, void *key,
+                      const void *value,
+                      void *key_cache, void *value_cache, const float *cos_table,
+                      const float *sin_table, const int32_t *positions,
+                      const int32_t *slot_mapping, int64_t num_tokens, int num_heads,
+                      int num_kv_heads, int head_dim, int64_t table_rows, int block_size,
+                      int64_t num_blocks, int64_t q_stride_tok, int64_t q_stride_head,
+                      int64_t k_stride_tok, int64_t k_stride_head, int64_t v_stride_tok,
+                      int64_t v_stride_head, void *stream);
+
+/*
  * Causal prefill attention over contiguous Q/K/V, GQA:
  *   out[b, s, h, :] = sum_{t <= s} softmax_t(scale * q[b,s,h] . k[b,t,g]) v[b,t,g]
  * with g = h / (num_heads / num_kv_heads).  query/out contiguous

@@ -20,6 +20,11 @@
 //   the same wave, so every K/V byte is read from HBM exactly once (the
 //   reference launches one warp per query head and reads each KV row G times).
 //   K/V are streamed with non-temporal loads (each byte is used once).
+//   Short contexts (capacity <= PER_SEQ_MAX_TOKENS) skip the split: the grid
+//   is one 8-wave workgroup per (kv head, sequence), the waves share the
+//   tiles of that head and merge in LDS, and the rows are written directly
+//   by a single kernel (the split's merge pass and its latency chain cost
+//   more than the few hundred KB each workgroup then streams).
 //   A sequence that lies inside one workgroup is normalised and written
 //   directly; otherwise each segment writes its partial softmax state (max m,
 //   sum l, unnormalised acc[128]) to the workspace and a second kernel merges
@@ -53,6 +58,8 @@ constexpr int MIN_BS = 8;
 constexpr int MAX_IDS = 2048;     // block ids staged in LDS at a time
 constexpr int MAX_BATCH = 2048;   // sequences per call (LDS prefix array)
 constexpr int MIN_TILES_PER_WG = 2;
+// Context capacities up to this many tokens take the per-sequence mode.
+constexpr int PER_SEQ_MAX_TOKENS = 1024;
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
@@ -68,6 +75,7 @@ struct DecodeArgs {
   int *ws_nparts;           // [B] workgroups covering each sequence
   int B, Hq, Hkv, maxb, bs_log2, J;
   int hpg, wph;             // kv heads per workgroup, waves per kv head
+  int per_seq;              // 1: workgroup (group, b) covers all of sequence b
   int64_t num_blocks;
   float scale_log2;
 };
@@ -89,17 +97,17 @@ __device__ int build_tile_prefix(const DecodeArgs &a, int *pre, int *wave_tot) {
       if (lane >= d) incl += o;
     }
     if (lane == 63) wave_tot[w] = incl;
-    __syncthreads();
+    lds_barrier();
     int before = carry;
     for (int ww = 0; ww < w; ++ww) before += wave_tot[ww];
     if (b < a.B) pre[b] = before + incl - v;
     int total = 0;
     for (int ww = 0; ww < DEC_NW; ++ww) total += wave_tot[ww];
     carry += total;
-    __syncthreads();
+    lds_barrier();
   }
   if (tid == 0) pre[a.B] = carry;
-  __syncthreads();
+  lds_barrier();
   return carry;
 }
 
@@ -142,9 +150,29 @@ void paged_decode_kernel(DecodeArgs a) {
   __shared__ float red_acc[DEC_NW][G][HD];
   __shared__ float red_m[DEC_NW][G], red_l[DEC_NW][G];
 
-  const int NT = build_tile_prefix(a, pre, wave_tot);
-  const int je = partition_count(NT, a.J);
-  if (j == 0) {
+  int NT, je;
+  if (a.per_seq) {
+    // one workgroup per (head group, sequence j): a one-sequence tile space
+    // [0, tiles of j), so the segment loop below runs once with nparts == 1
+    // and the rows are written directly (no merge pass)
+    if (tid == 0) {
+      pre[j] = 0;
+      pre[j + 1] = (clamp_ctx(a.ctx_lens[j], cap) + TILE - 1) / TILE;
+    }
+    lds_barrier();
+    NT = pre[j + 1];
+    je = 1;
+    if (NT == 0) {
+      const int h_lo = hgrp * hpg * G, h_hi = min(a.Hkv, (hgrp + 1) * hpg) * G;
+      for (int i = tid; i < (h_hi - h_lo) * HD; i += NT_THREADS)
+        a.out[((int64_t)j * a.Hq + h_lo) * HD + i] = 0;
+      return;
+    }
+  } else {
+    NT = build_tile_prefix(a, pre, wave_tot);
+    je = partition_count(NT, a.J);
+  }
+  if (!a.per_seq && j == 0) {
     // rows of empty sequences are zeros; workgroup 0 of each head group
     // writes them for its heads
     const int h_lo = hgrp * hpg * G, h_hi = min(a.Hkv, (hgrp + 1) * hpg) * G;
@@ -158,13 +186,14 @@ void paged_decode_kernel(DecodeArgs a) {
                              ? 0
                              : owner_of(pre[b + 1] - 1, NT, je) - owner_of(pre[b], NT, je) + 1;
   }
-  if (j >= je) return;
-  const int t_lo = range_start(j, NT, je), t_hi = range_start(j + 1, NT, je);
+  if (!a.per_seq && j >= je) return;
+  const int t_lo = a.per_seq ? 0 : range_start(j, NT, je);
+  const int t_hi = a.per_seq ? NT : range_start(j + 1, NT, je);
   if (t_lo >= t_hi) return;
 
   // first sequence whose tiles reach past t_lo
-  int b;
-  {
+  int b = j;
+  if (!a.per_seq) {
     int lo = 0, hi = a.B;
     while (lo < hi) {
       const int mid = (lo + hi) >> 1;
@@ -218,12 +247,12 @@ void paged_decode_kernel(DecodeArgs a) {
       const int t_end = min(s_lo + sub_tokens, tok_end);
       const int first_blk = s_lo >> bs_log2;
       const int nblk = ((t_end - 1) >> bs_log2) - first_blk + 1;
-      __syncthreads();  // previous users of blk_lds are done
+      lds_barrier();  // previous users of blk_lds are done
       for (int i = tid; i < nblk; i += NT_THREADS) {
         const int v = bt[first_blk + i];
         blk_lds[i] = v < 0 ? 0 : (v > nb_hi ? nb_hi : v);
       }
-      __syncthreads();
+      lds_barrier();
       if (!active) continue;
 
       // ---- loads of one tile: lane group lg owns tokens t0 + 8 lg .. +7 (one
@@ -385,7 +414,7 @@ void paged_decode_kernel(DecodeArgs a) {
       continue;
     }
     // several waves share a kv head: merge their states through LDS
-    __syncthreads();  // previous segment's readers of red_* are done
+    lds_barrier();  // previous segment's readers of red_* are done
     if (lg == 0) {
 #pragma unroll
       for (int h = 0; h < G; ++h) {
@@ -402,7 +431,7 @@ void paged_decode_kernel(DecodeArgs a) {
         red_l[w][h] = l_tot[h];
       }
     }
-    __syncthreads();
+    lds_barrier();
     const int nheads = min(hpg, a.Hkv - hgrp * hpg);
     for (int idx = tid; idx < nheads * G * HD; idx += NT_THREADS) {
       const int hh = idx / (G * HD), rem = idx - hh * G * HD;
@@ -450,12 +479,12 @@ __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
     const float li = d < cn ? ml[2 * (c0 + d) + 1] : 0.f;
     const float wm = wave_max(mi);
     if ((d & 63) == 0) mx_lds[d >> 6] = wm;
-    __syncthreads();
+    lds_barrier();
     const float m_new = fmaxf(M, fmaxf(mx_lds[0], mx_lds[1]));
     const float wi = d < cn ? fast_exp2(mi - m_new) : 0.f;
     w_lds[d] = wi;
     wl_lds[d] = wi * li;
-    __syncthreads();
+    lds_barrier();
     const float sc = fast_exp2(M - m_new);  // 0 on the first pass
     A *= sc;
     L *= sc;
@@ -475,7 +504,7 @@ __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
       L += wl_lds[i];
     }
     M = m_new;
-    __syncthreads();
+    lds_barrier();
   }
   a.out[row * HD + d] = F16T::from_float(A / L);
 }
@@ -584,10 +613,20 @@ extern "C" int mce_paged_attention_decode(
   a.J = Lay.J;
   a.hpg = Lay.hpg;
   a.wph = Lay.wph;
+  // Short contexts: one workgroup per (kv head, sequence) streams the whole
+  // sequence (at most PER_SEQ_MAX_TOKENS x 512 bytes of K/V) and writes the
+  // final rows, so the launch is one kernel with no partials.  Longer
+  // contexts use the balanced split over the concatenated tile space.
+  const bool per_seq = (int64_t)max_blocks_per_seq * block_size <= PER_SEQ_MAX_TOKENS;
+  a.per_seq = per_seq ? 1 : 0;
+  if (per_seq) {
+    a.hpg = 1;
+    a.wph = DEC_NW;
+  }
   a.num_blocks = num_blocks;
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid(Lay.groups, Lay.J);
+  const dim3 grid = per_seq ? dim3(num_kv_heads, batch) : dim3(Lay.groups, Lay.J);
 #define MCE_DEC_CASE(GG)                                                       \
   case GG:                                                                     \
     paged_decode_kernel<GG><<<grid, NT_THREADS, 0, st>>>(a);                   \
@@ -603,6 +642,6 @@ extern "C" int mce_paged_attention_decode(
     MCE_DEC_CASE(8)
   }
 #undef MCE_DEC_CASE
-  paged_decode_merge_kernel<<<dim3(num_heads, batch), HD, 0, st>>>(a);
+  if (!per_seq) paged_decode_merge_kernel<<<dim3(num_heads, batch), HD, 0, st>>>(a);
   return check_launch("mce_paged_attention_decode");
 }

@@ -27,7 +27,13 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(
   const int nvec = hidden >> 3;  // 8 elements per 16-byte vector
   const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + row * in_stride);
   const u32x4 *wr = reinterpret_cast<const u32x4 *>(w);
-  u32x4 v[VPT];
+  u32x4 v[VPT], wv[VPT];
+  // the weight loads go out with the row loads, ahead of the reduction
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    int idx = lane + i * 64;
+    if (idx < nvec) wv[i] = wr[idx];
+  }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
@@ -48,12 +54,11 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(
   for (int i = 0; i < VPT; ++i) {
     int idx = lane + i * 64;
     if (idx < nvec) {
-      u32x4 wv = wr[idx];
       u32x4 o;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        float a = T::lo(v[i][k]) * (inv * T::lo(wv[k]));
-        float b = T::hi(v[i][k]) * (inv * T::hi(wv[k]));
+        float a = T::lo(v[i][k]) * (inv * T::lo(wv[i][k]));
+        float b = T::hi(v[i][k]) * (inv * T::hi(wv[i][k]));
         o[k] = pack2<T>(a, b);
       }
       yr[idx] = o;
@@ -236,8 +241,8 @@ __global__ __launch_bounds__(256) void kv_store_generic_kernel(
 // share the launch (heads >= num_heads index K).
 // =========================================================================
 template <class T>
-__device__ inline void rope_rotate4(uint16_t *p, int half, const float *c4,
-                                    const float *s4) {
+__device__ inline void rope_rotate4(const uint16_t *p, int half, const float *c4,
+                                    const float *s4, uint16_t *out) {
   u32x2 a = *reinterpret_cast<const u32x2 *>(p);
   u32x2 b = *reinterpret_cast<const u32x2 *>(p + half);
   float x0[4] = {T::lo(a[0]), T::hi(a[0]), T::lo(a[1]), T::hi(a[1])};
@@ -253,8 +258,8 @@ __device__ inline void rope_rotate4(uint16_t *p, int half, const float *c4,
   oa[1] = pack2<T>(r0[2], r0[3]);
   ob[0] = pack2<T>(r1[0], r1[1]);
   ob[1] = pack2<T>(r1[2], r1[3]);
-  *reinterpret_cast<u32x2 *>(p) = oa;
-  *reinterpret_cast<u32x2 *>(p + half) = ob;
+  *reinterpret_cast<u32x2 *>(out) = oa;
+  *reinterpret_cast<u32x2 *>(out + half) = ob;
 }
 
 template <class T>
@@ -285,7 +290,80 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(
     floatx4 sn = *reinterpret_cast<const floatx4 *>(sin_t + ps * half + qd * 4);
     float c4[4] = {c[0], c[1], c[2], c[3]};
     float s4[4] = {sn[0], sn[1], sn[2], sn[3]};
-    rope_rotate4<T>(p + qd * 4, half, c4, s4);
+    rope_rotate4<T>(p + qd * 4, half, c4, s4, p + qd * 4);
+  }
+}
+
+// RoPE of q and k in place plus the paged store of the rotated k and of v,
+// in one launch (the engine applies rope_inplace and paged_kv_store back to
+// back on the same tokens).  One lane per 4 rotation pairs of one (token,
+// head): head slots [0, Hq) are query heads (rotated in place, or into the
+// contiguous [N, Hq, D] rows of q_out when given), [Hq, Hq + Hkv) key heads
+// (rotated in place, then written to key_cache[slot]), [Hq + Hkv, Hq + 2 Hkv)
+// value heads (copied to value_cache[slot]).  Same arithmetic as
+// rope_vec_kernel, so the results are bit-identical to the two separate ops;
+// positions outside the table leave q/k unrotated and slots outside the pool
+// are skipped, as in the separate ops.
+template <class T>
+__global__ __launch_bounds__(256) void rope_kv_store_vec_kernel(
+    uint16_t *__restrict__ q, uint16_t *__restrict__ q_out, uint16_t *__restrict__ k,
+    const uint16_t *__restrict__ v, uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+    const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+    const int32_t *__restrict__ pos, const int32_t *__restrict__ slots, int64_t tokens,
+    int num_heads, int num_kv_heads, int head_dim, int64_t table_rows, int64_t num_slots,
+    int64_t qst, int64_t qsh, int64_t kst, int64_t ksh, int64_t vst, int64_t vsh) {
+  const int half = head_dim >> 1;
+  const int quads = half >> 2;
+  const int heads = num_heads + 2 * num_kv_heads;
+  const int64_t per_tok = (int64_t)heads * quads;
+  const int64_t total = tokens * per_tok;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t t = i / per_tok;
+    const int rem = (int)(i - t * per_tok);
+    const int h = rem / quads, qd = rem - h * quads;
+    const int64_t ps = pos[t];
+    const bool in_table = ps >= 0 && ps < table_rows;
+    if (h < num_heads) {
+      const uint16_t *p = q + t * qst + h * qsh + qd * 4;
+      uint16_t *dst = q_out ? q_out + (t * num_heads + h) * head_dim + qd * 4
+                            : q + t * qst + h * qsh + qd * 4;
+      if (in_table) {
+        floatx4 c = *reinterpret_cast<const floatx4 *>(cos_t + ps * half + qd * 4);
+        floatx4 sn = *reinterpret_cast<const floatx4 *>(sin_t + ps * half + qd * 4);
+        float c4[4] = {c[0], c[1], c[2], c[3]};
+        float s4[4] = {sn[0], sn[1], sn[2], sn[3]};
+        rope_rotate4<T>(p, half, c4, s4, dst);
+      } else if (q_out) {
+        *reinterpret_cast<u32x2 *>(dst) = *reinterpret_cast<const u32x2 *>(p);
+        *reinterpret_cast<u32x2 *>(dst + half) = *reinterpret_cast<const u32x2 *>(p + half);
+      }
+      continue;
+    }
+    const int64_t sl = slots[t];
+    const bool store = sl >= 0 && sl < num_slots;
+    if (h < num_heads + num_kv_heads) {
+      const int hk = h - num_heads;
+      uint16_t *p = k + t * kst + hk * ksh + qd * 4;
+      if (in_table) {
+        floatx4 c = *reinterpret_cast<const floatx4 *>(cos_t + ps * half + qd * 4);
+        floatx4 sn = *reinterpret_cast<const floatx4 *>(sin_t + ps * half + qd * 4);
+        float c4[4] = {c[0], c[1], c[2], c[3]};
+        float s4[4] = {sn[0], sn[1], sn[2], sn[3]};
+        rope_rotate4<T>(p, half, c4, s4, p);
+      }
+      if (store) {
+        uint16_t *dst = kc + (sl * num_kv_heads + hk) * head_dim + qd * 4;
+        *reinterpret_cast<u32x2 *>(dst) = *reinterpret_cast<const u32x2 *>(p);
+        *reinterpret_cast<u32x2 *>(dst + half) = *reinterpret_cast<const u32x2 *>(p + half);
+      }
+    } else if (store) {
+      const int hv = h - num_heads - num_kv_heads;
+      const uint16_t *p = v + t * vst + hv * vsh + qd * 4;
+      uint16_t *dst = vc + (sl * num_kv_heads + hv) * head_dim + qd * 4;
+      *reinterpret_cast<u32x2 *>(dst) = *reinterpret_cast<const u32x2 *>(p);
+      *reinterpret_cast<u32x2 *>(dst + half) = *reinterpret_cast<const u32x2 *>(p + half);
+    }
   }
 }
 
@@ -448,4 +526,77 @@ extern "C" int mce_rope_inplace(int dtype, void *query, void *key,
       rope_generic_kernel<BF16T><<<grid_for(work), 256, 0, st>>>(q, k, cos_table, sin_table, positions, tokens, seq_len, num_heads, num_kv_heads, head_dim, table_rows, q_stride_b, q_stride_s, q_stride_h, k_stride_b, k_stride_s, k_stride_h);
   }
   return check_launch("mce_rope_inplace");
+}
+
+extern "C" int mce_rope_kv_store(int dtype, void *query, void *query_out, void *key,
+                                 const void *value,
+                                 void *key_cache, void *value_cache,
+                                 const float *cos_table, const float *sin_table,
+                                 const int32_t *positions, const int32_t *slot_mapping,
+                                 int64_t num_tokens, int num_heads, int num_kv_heads,
+                                 int head_dim, int64_t table_rows, int block_size,
+                                 int64_t num_blocks, int64_t q_stride_tok,
+                                 int64_t q_stride_head, int64_t k_stride_tok,
+                                 int64_t k_stride_head, int64_t v_stride_tok,
+                                 int64_t v_stride_head, void *stream) {
+  clear_error();
+  MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16, "mce_rope_kv_store: unknown dtype %d", dtype);
+  MCE_REQUIRE(num_tokens >= 0 && num_heads >= 0 && num_kv_heads >= 1 && head_dim >= 2 &&
+                  head_dim % 2 == 0 && table_rows >= 0 && block_size >= 1 && num_blocks >= 0,
+              "mce_rope_kv_store: bad shape");
+  if (num_tokens == 0) return MCE_OK;
+  MCE_REQUIRE(query && key && value && key_cache && value_cache && cos_table && sin_table &&
+                  positions && slot_mapping,
+              "mce_rope_kv_store: null pointer");
+  const int half = head_dim / 2;
+  const bool vec = half % 4 == 0 && q_stride_tok % 4 == 0 && q_stride_head % 4 == 0 &&
+                   (reinterpret_cast<uintptr_t>(query_out) & 7) == 0 &&
+                   k_stride_tok % 4 == 0 && k_stride_head % 4 == 0 && v_stride_tok % 4 == 0 &&
+                   v_stride_head % 4 == 0 && ((reinterpret_cast<uintptr_t>(query) |
+                                               reinterpret_cast<uintptr_t>(key) |
+                                               reinterpret_cast<uintptr_t>(value) |
+                                               reinterpret_cast<uintptr_t>(key_cache) |
+                                               reinterpret_cast<uintptr_t>(value_cache)) &
+                                              7) == 0 &&
+                   aligned16(cos_table) && aligned16(sin_table);
+  if (!vec) {
+    // any layout: the two separate ops (query rows copied out first)
+    if (query_out) {
+      const size_t row = (size_t)head_dim * 2;
+      for (int h = 0; h < num_heads; ++h)
+        if (hipMemcpy2DAsync((char *)query_out + h * row, (size_t)num_heads * row,
+                             (const char *)query + h * q_stride_head * 2,
+                             (size_t)q_stride_tok * 2, row, (size_t)num_tokens,
+                             hipMemcpyDeviceToDevice, (hipStream_t)stream) != hipSuccess)
+          return set_error(MCE_ERR_LAUNCH, "mce_rope_kv_store: query copy failed");
+      query = query_out;
+      q_stride_tok = (int64_t)num_heads * head_dim;
+      q_stride_head = head_dim;
+    }
+    int rc = mce_rope_inplace(dtype, query, key, cos_table, sin_table, positions,
+                              (int)num_tokens, 1, num_heads, num_kv_heads, head_dim, table_rows,
+                              q_stride_tok, 0, q_stride_head, k_stride_tok, 0, k_stride_head,
+                              stream);
+    if (rc != MCE_OK) return rc;
+    return mce_paged_kv_store(dtype, key, value, key_cache, value_cache, slot_mapping,
+                              num_tokens, num_kv_heads, head_dim, block_size, num_blocks,
+                              k_stride_tok, k_stride_head, v_stride_tok, v_stride_head, stream);
+  }
+  MCE_REQUIRE(num_tokens < ((int64_t)1 << 31), "mce_rope_kv_store: too many tokens");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t num_slots = num_blocks * block_size;
+  const int64_t work = num_tokens * (num_heads + 2 * num_kv_heads) * (half / 4);
+#define MCE_RKV(TT)                                                                              \
+  rope_kv_store_vec_kernel<TT><<<grid_for(work), 256, 0, st>>>(                                  \
+      (uint16_t *)query, (uint16_t *)query_out, (uint16_t *)key, (const uint16_t *)value,        \
+      (uint16_t *)key_cache,                                                                     \
+      (uint16_t *)value_cache, cos_table, sin_table, positions, slot_mapping, num_tokens,        \
+      num_heads, num_kv_heads, head_dim, table_rows, num_slots, q_stride_tok, q_stride_head,     \
+      k_stride_tok, k_stride_head, v_stride_tok, v_stride_head)
+  if (dtype == MCE_F16)
+    MCE_RKV(F16T);
+  else
+    MCE_RKV(BF16T);
+#undef MCE_RKV
+  return check_launch("mce_rope_kv_store");
 }

@@ -17,7 +17,11 @@ matrix, so a layer runs 4 GEMMs instead of 7 and SwiGLU reads the gate/up
 GEMM output directly (the reference concatenates gate and up activations
 with torch.cat every step, llama.py:161).  The original weight names stay
 in `weights` as views into the fused matrices.  q/k/v are strided views of
-the fused projection output; RoPE and the KV store take them in place.
+the fused projection output; one fused launch rotates q (into a contiguous
+buffer for the attention kernel) and k and writes k/v to their pages (the
+reference calls rope_inplace and paged_kv_store, llama.py:117-127), and the
+o_proj / down_proj GEMMs add into the residual stream in place (addmm_)
+instead of a separate add.
 RoPE tables cover max_position_embeddings positions (capped at 131072)
 instead of the reference's fixed 4096 (llama.py:42).
 """
@@ -30,6 +34,7 @@ import torch
 
 import my_cuda_engine_cpp as ops
 
+from ...ops import rope_kv_store
 from ..cache import KVCacheManager
 
 ROPE_TABLE_CAP = 131072
@@ -106,12 +111,14 @@ class Llama3BEngineModel:
         v = qkv[:, (hq + hkv) * d:]
         return q, k, v
 
-    def _mlp(self, l: int, x: torch.Tensor) -> torch.Tensor:
+    def _mlp(self, l: int, x: torch.Tensor) -> None:
+        """x += down(SwiGLU(gate_up(RMSNorm(x)))), the residual add done by the
+        down-projection GEMM (addmm_ accumulates into x)."""
         p = f"model.layers.{l}"
         xn = ops.rmsnorm(x, self.weights[f"{p}.post_attention_layernorm.weight"],
                          self.config.rms_norm_eps)
         act = ops.swiglu(torch.matmul(xn, self.w_gate_up[l].T))
-        return x + torch.matmul(act, self.weights[f"{p}.mlp.down_proj.weight"].T)
+        x.addmm_(act, self.weights[f"{p}.mlp.down_proj.weight"].T)
 
     def decode_step(self, input_ids: torch.Tensor, positions: torch.Tensor,
                     context_lens: torch.Tensor, slot_mapping: torch.Tensor,
@@ -126,16 +133,15 @@ class Llama3BEngineModel:
             p = f"model.layers.{l}"
             xn = ops.rmsnorm(x, self.weights[f"{p}.input_layernorm.weight"], c.rms_norm_eps)
             q, k, v = self._attention_block_proj(l, xn)
-            ops.rope_inplace(q.view(b, 1, hq, d), k.view(b, 1, hkv, d), self.cos_table,
-                             self.sin_table, positions)
-            ops.paged_kv_store(k.view(b, hkv, d), v.view(b, hkv, d), kv[l, 0], kv[l, 1],
-                               slot_mapping)
-            attn = ops.paged_attention_decode(q.view(b, hq, d), kv[l, 0], kv[l, 1],
+            q_rot = torch.empty(b, hq, d, dtype=q.dtype, device=q.device)
+            rope_kv_store(q.view(b, hq, d), k.view(b, hkv, d), v.view(b, hkv, d), kv[l, 0],
+                          kv[l, 1], self.cos_table, self.sin_table, positions.view(-1),
+                          slot_mapping, query_out=q_rot)
+            attn = ops.paged_attention_decode(q_rot, kv[l, 0], kv[l, 1],
                                               block_tables_tensor, context_lens,
                                               max_blocks_per_seq,
                                               self.cache_manager.block_size, self.scale)
-            x = x + torch.matmul(attn.view(b, hq * d),
-                                 self.weights[f"{p}.self_attn.o_proj.weight"].T)
-            x = self._mlp(l, x)
+            x.addmm_(attn.view(b, hq * d), self.weights[f"{p}.self_attn.o_proj.weight"].T)
+            self._mlp(l, x)
         xf = ops.rmsnorm(x, self.weights["model.norm.weight"], c.rms_norm_eps)
         return torch.matmul(xf, self.lm_head.T)

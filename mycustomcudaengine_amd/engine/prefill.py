@@ -2,7 +2,7 @@
 
 prefill_step(model, input_ids [B, S], seq_ids, context_lens) -> last-token
 logits [B, vocab].  Per layer: RMSNorm -> fused q/k/v projection -> RoPE in
-place (positions 0..S-1) -> paged KV store of all B*S tokens in ONE launch ->
+place (positions 0..S-1) and the paged KV store of all B*S tokens in ONE launch ->
 causal prefill attention on the contiguous q/k/v -> o_proj + residual ->
 RMSNorm -> fused gate/up -> SwiGLU -> down + residual; then the final
 RMSNorm and lm_head on the last position only (benchmark_engine.py:124-127).
@@ -24,6 +24,8 @@ import torch
 
 import my_cuda_engine_cpp as ops
 
+from ..ops import rope_kv_store
+
 
 def prefill_step(model, input_ids: torch.Tensor, seq_ids: List[int],
                  context_lens: torch.Tensor = None) -> torch.Tensor:
@@ -41,12 +43,12 @@ def prefill_step(model, input_ids: torch.Tensor, seq_ids: List[int],
         xn = ops.rmsnorm(x, model.weights[f"{p}.input_layernorm.weight"], c.rms_norm_eps)
         q, k, v = model._attention_block_proj(l, xn)
         q4, k4, v4 = q.view(b, s, hq, d), k.view(b, s, hkv, d), v.view(b, s, hkv, d)
-        ops.rope_inplace(q4, k4, model.cos_table, model.sin_table, positions)
-        ops.paged_kv_store(k.view(b * s, hkv, d), v.view(b * s, hkv, d), kv[l, 0], kv[l, 1], slots)
+        rope_kv_store(q.view(b * s, hq, d), k.view(b * s, hkv, d), v.view(b * s, hkv, d),
+                      kv[l, 0], kv[l, 1], model.cos_table, model.sin_table,
+                      positions.view(-1), slots)
         attn = ops.prefill_attention(q4, k4, v4, model.scale)  # [B, S, Hq, D]
-        x = x + torch.matmul(attn.view(b * s, hq * d),
-                             model.weights[f"{p}.self_attn.o_proj.weight"].T)
-        x = model._mlp(l, x)
+        x.addmm_(attn.view(b * s, hq * d), model.weights[f"{p}.self_attn.o_proj.weight"].T)
+        model._mlp(l, x)
     last = x.view(b, s, -1)[:, -1].contiguous()
     xf = ops.rmsnorm(last, model.weights["model.norm.weight"], c.rms_norm_eps)
     return torch.matmul(xf, model.lm_head.T)

@@ -235,6 +235,60 @@ def rope_inplace(query: torch.Tensor, key, cos_table: torch.Tensor,
                   ks[0], ks[1], ks[2], _stream(dev))
 
 
+def rope_kv_store(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                  key_cache: torch.Tensor, value_cache: torch.Tensor,
+                  cos_table: torch.Tensor, sin_table: torch.Tensor, positions: torch.Tensor,
+                  slot_mapping: torch.Tensor, query_out: torch.Tensor = None) -> None:
+    """rope_inplace(query, key) then paged_kv_store(key, value) in one launch.
+
+    Engine-side fusion of the two calls the reference decode step makes back
+    to back (engine/models/llama.py:117-127); identical results.  query
+    [N, Hq, D], key/value [N, Hkv, D] (any token/head strides, contiguous last
+    dim); caches contiguous [num_blocks, block_size, Hkv, D]; cos/sin fp32
+    [P, D/2]; positions and slot_mapping contiguous int32 [N].  With
+    query_out (contiguous [N, Hq, D]) the rotated query is written there and
+    query is left as it was.
+    """
+    dev = _on_gpu("rope_kv_store", query, key, value, key_cache, value_cache, cos_table,
+                  sin_table, positions, slot_mapping)
+    code = _dtype_code(query, "rope_kv_store query")
+    for t, n in ((key, "key"), (value, "value"), (key_cache, "key_cache"),
+                 (value_cache, "value_cache")):
+        _check(t.dtype == query.dtype, f"rope_kv_store: {n} dtype must match query")
+    _check(query.dim() == 3 and key.dim() == 3 and value.shape == key.shape and
+           key.size(0) == query.size(0) and key.size(2) == query.size(2),
+           "rope_kv_store: query [N, Hq, D], key/value [N, Hkv, D] expected")
+    n_tok, hq, d = query.shape
+    hkv = key.size(1)
+    _check(d % 2 == 0, f"rope_kv_store: head_dim must be even (got {d})")
+    for t, n in ((query, "query"), (key, "key"), (value, "value")):
+        _check(t.stride(-1) == 1, f"rope_kv_store: {n} last dim must be contiguous")
+    _check(key_cache.dim() == 4 and key_cache.shape == value_cache.shape and
+           key_cache.size(2) == hkv and key_cache.size(3) == d and
+           key_cache.is_contiguous() and value_cache.is_contiguous(),
+           "rope_kv_store: caches must be contiguous [num_blocks, block_size, Hkv, D]")
+    nb, bs = key_cache.shape[:2]
+    for t, n in ((cos_table, "cos_table"), (sin_table, "sin_table")):
+        _check(t.dtype == torch.float32 and t.dim() == 2 and t.size(1) == d // 2 and
+               t.is_contiguous(), f"rope_kv_store: {n} must be contiguous fp32 [P, {d // 2}]")
+    _check(cos_table.size(0) == sin_table.size(0), "rope_kv_store: table lengths differ")
+    for t, n in ((positions, "positions"), (slot_mapping, "slot_mapping")):
+        _check(t.dtype == torch.int32 and t.numel() == n_tok and t.is_contiguous(),
+               f"rope_kv_store: {n} must be contiguous int32 with {n_tok} elements")
+    if query_out is not None:
+        _check(query_out.dtype == query.dtype and query_out.shape == query.shape and
+               query_out.is_contiguous() and query_out.device == query.device,
+               "rope_kv_store: query_out must be a contiguous tensor like query")
+    with _on_device(dev):
+        _lib.call("mce_rope_kv_store", code, query.data_ptr(),
+                  query_out.data_ptr() if query_out is not None else None, key.data_ptr(),
+                  value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+                  cos_table.data_ptr(), sin_table.data_ptr(), positions.data_ptr(),
+                  slot_mapping.data_ptr(), n_tok, hq, hkv, d, cos_table.size(0), bs, nb,
+                  query.stride(0), query.stride(1), key.stride(0), key.stride(1),
+                  value.stride(0), value.stride(1), _stream(dev))
+
+
 def prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                       scale: float) -> torch.Tensor:
     """Causal GQA attention on contiguous Q/K/V (reference: prefill_attention.cu:271-309).

@@ -15,6 +15,7 @@ HEADER_ENTRY_POINTS = {
     "mce_last_error", "mce_abi_version", "mce_rmsnorm", "mce_swiglu",
     "mce_paged_kv_store", "mce_paged_attention_decode_workspace_size",
     "mce_paged_attention_decode", "mce_rope_inplace", "mce_prefill_attention",
+    "mce_rope_kv_store",
 }
 
 
@@ -23,7 +24,7 @@ def lib():
     return _lib.load()
 
 
-def test_header_declares_the_six_ops_and_helpers():
+def test_header_declares_the_six_ops_fused_op_and_helpers():
     assert set(_lib.header_symbols()) == HEADER_ENTRY_POINTS
 
 
@@ -111,6 +112,18 @@ def test_rope_and_prefill_validation(lib):
                                      None) == _lib.MCE_ERR_INVALID
     assert lib.mce_prefill_attention(0, None, None, None, None, 0, 8, 24, 8, 128, 0.1,
                                      None) == _lib.MCE_OK
+
+
+def test_rope_kv_store_validation(lib):
+    f = lib.mce_rope_kv_store
+    args = [0] + [None] * 10 + [4, 24, 8, 128, 4096, 16, 10, 0, 0, 0, 0, 0, 0, None]
+    assert f(*args) == _lib.MCE_ERR_INVALID and "null" in _err(lib)
+    bad = list(args); bad[0] = 5
+    assert f(*bad) == _lib.MCE_ERR_INVALID and "dtype" in _err(lib)
+    odd = list(args); odd[14] = 127
+    assert f(*odd) == _lib.MCE_ERR_INVALID
+    empty = list(args); empty[11] = 0
+    assert f(*empty) == _lib.MCE_OK
 
 
 def test_python_ops_reject_cpu_tensors():

@@ -199,6 +199,70 @@ def test_prefill_first_row_is_v0(dev):
     assert (out[0, 0].float() - v0).abs().max().item() <= 2e-3 * (1 + v0.abs().max().item())
 
 
+@pytest.mark.parametrize("n_tok,hq,hkv,strided", [(8, 24, 8, True), (74, 24, 8, False),
+                                                   (5, 6, 2, True)])
+def test_rope_kv_store_equals_separate_ops(dev, n_tok, hq, hkv, strided):
+    """The engine's fused RoPE + paged store gives the same bits as rope_inplace
+    followed by paged_kv_store, and both match the oracle: strided q/k/v views
+    of one fused projection row (rotated q written to a separate contiguous
+    query_out), an out-of-table position (left unrotated) and invalid slots
+    (-1, past the pool: skipped)."""
+    from mycustomcudaengine_amd.ops import rope_kv_store
+    d, nb, bs = 128, 12, 16
+    g = gen(70 + n_tok)
+    if strided:
+        qkv = torch.randn(n_tok, (hq + 2 * hkv) * d, generator=g).half()
+        q0 = qkv[:, : hq * d].view(n_tok, hq, d)
+        k0 = qkv[:, hq * d:(hq + hkv) * d].view(n_tok, hkv, d)
+        v0 = qkv[:, (hq + hkv) * d:].view(n_tok, hkv, d)
+    else:
+        q0 = torch.randn(n_tok, hq, d, generator=g).half()
+        k0 = torch.randn(n_tok, hkv, d, generator=g).half()
+        v0 = torch.randn(n_tok, hkv, d, generator=g).half()
+    cos, sin = rope_tables(64, d, 500000.0)
+    pos = torch.randint(0, 64, (n_tok,), generator=g, dtype=torch.int32)
+    pos[1] = 64  # outside the table
+    slots = torch.randperm(nb * bs, generator=g)[:n_tok].to(torch.int32)
+    slots[0] = -1
+    slots[-1] = nb * bs + 3
+    caches = []
+    for fused in (True, False):
+        base = qkv.clone().to(dev) if strided else None
+        if strided:
+            q = base[:, : hq * d].view(n_tok, hq, d)
+            k = base[:, hq * d:(hq + hkv) * d].view(n_tok, hkv, d)
+            v = base[:, (hq + hkv) * d:].view(n_tok, hkv, d)
+        else:
+            q, k, v = q0.clone().to(dev), k0.clone().to(dev), v0.clone().to(dev)
+        kc = torch.full((nb, bs, hkv, d), 7.0, dtype=torch.float16, device=dev)
+        vc = torch.full_like(kc, -3.0)
+        if fused:
+            q_out = torch.empty(n_tok, hq, d, dtype=torch.float16, device=dev) if strided else None
+            q_before = q.clone()
+            rope_kv_store(q, k, v, kc, vc, cos.to(dev), sin.to(dev), pos.to(dev), slots.to(dev),
+                          query_out=q_out)
+            if strided:  # rotated q went to q_out; the strided view is untouched
+                assert torch.equal(q, q_before)
+                q = q_out
+        else:
+            ops.rope_inplace(q.view(n_tok, 1, hq, d), k.view(n_tok, 1, hkv, d), cos.to(dev),
+                             sin.to(dev), pos.view(n_tok, 1).to(dev))
+            ops.paged_kv_store(k, v, kc, vc, slots.to(dev))
+        caches.append((q.cpu(), k.cpu(), kc.cpu(), vc.cpu()))
+    for a, b in zip(*caches):
+        assert torch.equal(a, b)
+    inside = torch.arange(n_tok) != 1  # the oracle's tables end at position 63
+    q_ref = rope_ref(q0[inside].view(-1, 1, hq, d), cos, sin,
+                     pos[inside].view(-1, 1)).view(-1, hq, d)
+    assert rel_close(caches[0][0][inside], q_ref, 4e-3, 2e-3)[0]
+    assert torch.equal(caches[0][0][1], q0[1])  # out-of-table position untouched
+    kr = torch.full((nb, bs, hkv, d), 7.0, dtype=torch.float16).numpy()
+    vr = torch.full((nb, bs, hkv, d), -3.0, dtype=torch.float16).numpy()
+    kv_store_ref(caches[0][1].numpy(), v0.numpy(), kr, vr, slots.numpy())
+    assert torch.equal(caches[0][2], torch.from_numpy(kr))
+    assert torch.equal(caches[0][3], torch.from_numpy(vr))
+
+
 def test_cfg3_rope_kvstore_prefill_pipeline(dev):
     """cfg3: RoPE (theta 5e5, positions 0..2047) in place, all 2048 K/V rows
     into 16-token pages of a permuted table (bit-exact), then causal attention."""
