@@ -3,12 +3,13 @@
 //
 // Work decomposition: balanced split-K (flash-decoding) over the whole batch.
 //   Every sequence's context is cut into 32-token tiles and the tiles of all
-//   sequences are laid end to end (sequence b owns tiles [pre[b], pre[b+1])).
+//   sequences are laid end to end (sequence b owns tiles [pre[b], pre[b+1]),
+//   the first SEG_TILES of them virtual: they weight the cost of a segment).
 //   The grid has J workgroups per group of kv heads (about one workgroup per
 //   CU in total) and workgroup j takes the contiguous tile range
-//   [j NT / J, (j+1) NT / J): every workgroup streams the same number of KV
-//   bytes whatever the mix of context lengths, so there is no tail of short
-//   chunks.  A range may cover the end of one sequence and the start of the
+//   [j NT / J, (j+1) NT / J): every workgroup gets the same split weight
+//   (streamed tiles plus segment starts) whatever the mix of context
+//   lengths, so there is no tail of short chunks.  A range may cover the end of one sequence and the start of the
 //   next; each such piece ("segment") is reduced separately.
 //   A workgroup has 8 waves and covers up to 8 kv heads of its tile range:
 //   wave w works on kv head w % HPG (HPG = heads per workgroup) and on every
@@ -58,6 +59,12 @@ constexpr int MIN_BS = 8;
 constexpr int MAX_IDS = 2048;     // block ids staged in LDS at a time
 constexpr int MAX_BATCH = 2048;   // sequences per call (LDS prefix array)
 constexpr int MIN_TILES_PER_WG = 2;
+// Split weight of a sequence start, in tiles: starting a segment (query and
+// block-id loads, pipeline refill, one more partial) costs one to two tiles of
+// streaming, so every non-empty sequence is preceded by SEG_TILES virtual
+// tiles in the split space and a workgroup that takes a boundary gets that
+// many fewer real tiles.
+constexpr int SEG_TILES = 1;
 // Context capacities up to this many tokens take the per-sequence mode.
 constexpr int PER_SEQ_MAX_TOKENS = 1024;
 
@@ -82,14 +89,17 @@ struct DecodeArgs {
 
 __device__ inline int clamp_ctx(int c, int cap) { return c < 0 ? 0 : (c > cap ? cap : c); }
 
-// Exclusive prefix sum of per-sequence tile counts into pre[0..B]; returns NT.
+// Exclusive prefix sum of per-sequence split weights (tiles + SEG_TILES for a
+// non-empty sequence) into pre[0..B]; returns NT.  Sequence b's real tiles
+// are [pre[b] + SEG_TILES, pre[b+1]).
 __device__ int build_tile_prefix(const DecodeArgs &a, int *pre, int *wave_tot) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int cap = a.maxb << a.bs_log2;
   int carry = 0;
   for (int base = 0; base < a.B; base += NT_THREADS) {
     const int b = base + tid;
-    const int v = b < a.B ? (clamp_ctx(a.ctx_lens[b], cap) + TILE - 1) / TILE : 0;
+    int v = b < a.B ? (clamp_ctx(a.ctx_lens[b], cap) + TILE - 1) / TILE : 0;
+    if (v > 0) v += SEG_TILES;
     int incl = v;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
@@ -150,8 +160,9 @@ void paged_decode_kernel(DecodeArgs a) {
   __shared__ float red_acc[DEC_NW][G][HD];
   __shared__ float red_m[DEC_NW][G], red_l[DEC_NW][G];
 
-  int NT, je;
+  int NT, je, seg0;  // seg0: virtual tiles at the start of each sequence
   if (a.per_seq) {
+    seg0 = 0;
     // one workgroup per (head group, sequence j): a one-sequence tile space
     // [0, tiles of j), so the segment loop below runs once with nparts == 1
     // and the rows are written directly (no merge pass)
@@ -169,6 +180,7 @@ void paged_decode_kernel(DecodeArgs a) {
       return;
     }
   } else {
+    seg0 = SEG_TILES;
     NT = build_tile_prefix(a, pre, wave_tot);
     je = partition_count(NT, a.J);
   }
@@ -184,7 +196,8 @@ void paged_decode_kernel(DecodeArgs a) {
       for (int b = tid; b < a.B; b += NT_THREADS)
         a.ws_nparts[b] = pre[b + 1] == pre[b]
                              ? 0
-                             : owner_of(pre[b + 1] - 1, NT, je) - owner_of(pre[b], NT, je) + 1;
+                             : owner_of(pre[b + 1] - 1, NT, je) -
+                                   owner_of(pre[b] + seg0, NT, je) + 1;
   }
   if (!a.per_seq && j >= je) return;
   const int t_lo = a.per_seq ? 0 : range_start(j, NT, je);
@@ -208,13 +221,14 @@ void paged_decode_kernel(DecodeArgs a) {
   const int nb_hi = (int)(a.num_blocks - 1 < 0x7fffffff ? a.num_blocks - 1 : 0x7fffffff);
 
   for (; b < a.B && pre[b] < t_hi; ++b) {
-    if (pre[b + 1] == pre[b]) continue;
+    const int r0 = pre[b] + seg0;  // first real tile of b in the split space
+    if (pre[b + 1] == pre[b] || max(t_lo, r0) >= min(t_hi, pre[b + 1])) continue;
     const int ctx = clamp_ctx(a.ctx_lens[b], cap);
-    const int seg_lo = max(t_lo, pre[b]) - pre[b];             // tile index in b
-    const int seg_hi = min(t_hi, pre[b + 1]) - pre[b];
+    const int seg_lo = max(t_lo, r0) - r0;             // tile index in b
+    const int seg_hi = min(t_hi, pre[b + 1]) - r0;
     const int tok_lo = seg_lo * TILE;
     const int tok_end = min(seg_hi * TILE, ctx);
-    const int j_first = owner_of(pre[b], NT, je);
+    const int j_first = owner_of(r0, NT, je);
     const int nparts = owner_of(pre[b + 1] - 1, NT, je) - j_first + 1;
 
     // This lane's slice of each query head: dims 8 lr .. 8 lr + 7 as packed
