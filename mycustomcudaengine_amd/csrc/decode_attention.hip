@@ -480,17 +480,30 @@ void paged_decode_kernel(DecodeArgs a) {
 // independent (unrolled) loads.
 __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int n = a.ws_nparts[b];
-  if (n <= 1) return;
-  __shared__ float w_lds[HD], wl_lds[HD], mx_lds[2];
   const int64_t row = (int64_t)b * a.Hq + h;
   const float *ml = a.ws_ml + row * a.J * 2;
   const float *ac = a.ws_acc + row * a.J * HD + d;
+  // The part count and the first HD parts' (m, l) are loaded together (one
+  // memory round trip); slots at or past the count are ignored (the
+  // workspace holds J >= parts slots per row, so these reads stay inside it).
+  const int n_raw = a.ws_nparts[b];
+  const float2 ml0 = d < a.J ? *reinterpret_cast<const float2 *>(ml + 2 * d) : float2{0.f, 0.f};
+  const int n = __builtin_amdgcn_readfirstlane(n_raw);
+  if (n <= 1) return;
+  __shared__ float w_lds[HD], wl_lds[HD], mx_lds[2];
   float M = -INFINITY, L = 0.f, A = 0.f;
   for (int c0 = 0; c0 < n; c0 += HD) {
     const int cn = min(HD, n - c0);
-    const float mi = d < cn ? ml[2 * (c0 + d)] : -INFINITY;
-    const float li = d < cn ? ml[2 * (c0 + d) + 1] : 0.f;
+    float mi = -INFINITY, li = 0.f;
+    if (d < cn) {
+      if (c0 == 0) {
+        mi = ml0.x;
+        li = ml0.y;
+      } else {
+        mi = ml[2 * (c0 + d)];
+        li = ml[2 * (c0 + d) + 1];
+      }
+    }
     const float wm = wave_max(mi);
     if ((d & 63) == 0) mx_lds[d >> 6] = wm;
     lds_barrier();
