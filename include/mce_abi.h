@@ -44,6 +44,9 @@ enum {
 
 enum { MCE_F16 = 0, MCE_BF16 = 1 };
 
+/* Epilogues of mce_decode_gemm. */
+enum { MCE_EPI_STORE = 0, MCE_EPI_ADD = 1, MCE_EPI_SWIGLU = 2 };
+
 /* Message of the last failed call on this host thread ("" if none). */
 MCE_API const char *mce_last_error(void);
 
@@ -171,6 +174,24 @@ MCE_API int mce_rope_kv_store(int dtype, void *query, void *query_out, void *key
                       int64_t num_blocks, int64_t q_stride_tok, int64_t q_stride_head,
                       int64_t k_stride_tok, int64_t k_stride_head, int64_t v_stride_tok,
                       int64_t v_stride_head, void *stream);
+
+/*
+ * Decode-sized projection: out[m, :n] (op)= x[m, :k] . w[:n, :k]^T for m <= 16
+ * rows (one token per sequence), w row-major [n, k] (the Hugging Face
+ * [out_features, in_features] layout), fp32 accumulation:
+ *   MCE_EPI_STORE  out = x w^T
+ *   MCE_EPI_ADD    out += x w^T            (in-place residual add)
+ *   MCE_EPI_SWIGLU w is [2n, k] (gate rows, then up rows);
+ *                  out[:, j] = silu(x w_gate_j) * (x w_up_j)
+ * x rows x_stride elements apart, out rows out_stride apart.  Needs
+ * n % 16 == 0, k a multiple of 512 with k / 512 <= 16 (<= 8 for SwiGLU);
+ * other shapes return MCE_ERR_UNSUPPORTED (callers then use a library GEMM).
+ * No single counterpart in the reference: its decode step runs these
+ * projections through torch.matmul, then a separate SwiGLU kernel and
+ * residual adds (engine/models/llama.py:94-110,143-165,174).
+ */
+MCE_API int mce_decode_gemm(int dtype, const void *x, const void *w, void *out, int m, int n,
+                    int k, int64_t x_stride, int64_t out_stride, int epilogue, void *stream);
 
 /*
  * Causal prefill attention over contiguous Q/K/V, GQA:

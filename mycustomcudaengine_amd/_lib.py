@@ -48,6 +48,8 @@ SIGNATURES = {
                                   _c_i64, _c_i64, _vp]),
     "mce_prefill_attention": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int,
                                        _c_int, _c_int, _c_f, _vp]),
+    "mce_decode_gemm": (_c_int, [_c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_i64, _c_i64,
+                                 _c_int, _vp]),
     "mce_rope_kv_store": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
                                    _c_i64, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_i64,
                                    _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _vp]),

@@ -25,6 +25,7 @@ SOURCES = [
     "elementwise.hip",
     "decode_attention.hip",
     "prefill_attention.hip",
+    "decode_gemm.hip",
 ]
 ARCH = "gfx950"
 

@@ -289,6 +289,47 @@ def rope_kv_store(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                   value.stride(0), value.stride(1), _stream(dev))
 
 
+_EPILOGUES = {"store": 0, "add": 1, "swiglu": 2}
+
+
+def decode_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None,
+                epilogue: str = "store") -> torch.Tensor:
+    """Decode-sized projection out (op)= x . weight^T for at most 16 rows.
+
+    x [M, K] (rows may be strided, contiguous last dim), weight contiguous
+    [N, K] ([2N, K] gate rows then up rows for "swiglu").  epilogue "store"
+    writes a new (or the given) [M, N] tensor; "add" accumulates into `out`
+    in place (residual stream); "swiglu" returns silu(x W_gate^T) * x W_up^T.
+    Raises MCEError with code MCE_ERR_UNSUPPORTED for shapes the kernel does
+    not take (M > 16, N % 16, K not a multiple of 512); the engine then uses
+    torch.matmul.  Engine-side op: the reference runs these projections
+    through torch.matmul (engine/models/llama.py:94-174).
+    """
+    dev = _on_gpu("decode_gemm", x, weight)
+    code = _dtype_code(x, "decode_gemm x")
+    _check(weight.dtype == x.dtype, "decode_gemm: weight dtype must match x")
+    _check(x.dim() == 2 and weight.dim() == 2 and x.size(1) == weight.size(1),
+           f"decode_gemm: x [M, K] and weight [N, K] expected (got {tuple(x.shape)}, "
+           f"{tuple(weight.shape)})")
+    _check(epilogue in _EPILOGUES, f"decode_gemm: unknown epilogue {epilogue!r}")
+    _check(x.stride(1) == 1 and weight.is_contiguous(),
+           "decode_gemm: x last dim and weight must be contiguous")
+    m, k = x.shape
+    n = weight.size(0) // 2 if epilogue == "swiglu" else weight.size(0)
+    _check(epilogue != "swiglu" or weight.size(0) % 2 == 0,
+           "decode_gemm: swiglu weight needs an even number of rows")
+    if out is None:
+        _check(epilogue != "add", "decode_gemm: epilogue 'add' needs out")
+        out = torch.empty(m, n, dtype=x.dtype, device=x.device)
+    _check(out.dtype == x.dtype and out.dim() == 2 and tuple(out.shape) == (m, n) and
+           out.stride(1) == 1 and out.device == x.device,
+           f"decode_gemm: out must be [{m}, {n}] with a contiguous last dim")
+    with _on_device(dev):
+        _lib.call("mce_decode_gemm", code, x.data_ptr(), weight.data_ptr(), out.data_ptr(),
+                  m, n, k, x.stride(0), out.stride(0), _EPILOGUES[epilogue], _stream(dev))
+    return out
+
+
 def prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                       scale: float) -> torch.Tensor:
     """Causal GQA attention on contiguous Q/K/V (reference: prefill_attention.cu:271-309).

@@ -15,7 +15,7 @@ HEADER_ENTRY_POINTS = {
     "mce_last_error", "mce_abi_version", "mce_rmsnorm", "mce_swiglu",
     "mce_paged_kv_store", "mce_paged_attention_decode_workspace_size",
     "mce_paged_attention_decode", "mce_rope_inplace", "mce_prefill_attention",
-    "mce_rope_kv_store",
+    "mce_rope_kv_store", "mce_decode_gemm",
 }
 
 
@@ -24,7 +24,7 @@ def lib():
     return _lib.load()
 
 
-def test_header_declares_the_six_ops_fused_op_and_helpers():
+def test_header_declares_the_six_ops_engine_ops_and_helpers():
     assert set(_lib.header_symbols()) == HEADER_ENTRY_POINTS
 
 
@@ -124,6 +124,20 @@ def test_rope_kv_store_validation(lib):
     assert f(*odd) == _lib.MCE_ERR_INVALID
     empty = list(args); empty[11] = 0
     assert f(*empty) == _lib.MCE_OK
+
+
+def test_decode_gemm_validation(lib):
+    f = lib.mce_decode_gemm
+    assert f(0, None, None, None, 8, 64, 512, 512, 64, 0, None) == _lib.MCE_ERR_INVALID
+    assert "null" in _err(lib)
+    assert f(0, None, None, None, 8, 64, 512, 512, 64, 7, None) == _lib.MCE_ERR_INVALID
+    assert f(0, None, None, None, 17, 64, 512, 512, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(0, None, None, None, 8, 60, 512, 512, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(0, None, None, None, 8, 64, 500, 512, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(0, None, None, None, 8, 64, 8704, 8704, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(0, None, None, None, 8, 64, 8192, 8192, 64, 2, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(1, None, None, None, 8, 64, 512, 512, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(0, None, None, None, 0, 64, 512, 512, 64, 0, None) == _lib.MCE_OK
 
 
 def test_python_ops_reject_cpu_tensors():

@@ -290,3 +290,49 @@ def test_cfg3_rope_kvstore_prefill_pipeline(dev):
     ref = prefill_attention_ref(q.cpu(), k.cpu(), v.cpu(), case.scale)
     err = (out.float() - ref).abs().max().item()
     assert err <= TOL, err
+
+
+# ------------------------------------------------------- decode-sized GEMM
+@pytest.mark.parametrize("m", [1, 5, 8, 16])
+@pytest.mark.parametrize("n,k,epi", [(5120, 3072, "store"), (3072, 3072, "add"),
+                                     (8192, 3072, "swiglu"), (3072, 8192, "add"),
+                                     (1024, 512, "store")])
+def test_decode_gemm_matches_fp32(dev, m, n, k, epi):
+    """x . W^T for the decode step's projection shapes with the fused
+    epilogues, against fp32 torch on the same fp16 inputs: plain store,
+    in-place residual add (o_proj / down_proj), SwiGLU over the fused
+    [gate; up] weight (gate_up + SwiGLU).  x rows are strided (a view into a
+    wider buffer) as the engine passes them."""
+    from mycustomcudaengine_amd.ops import decode_gemm
+    g = gen(80 + m + n // 512)
+    rows = 2 * n if epi == "swiglu" else n
+    xbuf = torch.randn(m, k + 64, generator=g).half()
+    x = xbuf[:, 32:32 + k]
+    w = (torch.randn(rows, k, generator=g) * 0.02).half()
+    acc = x.float() @ w.float().T
+    if epi == "swiglu":
+        gt, up = acc[:, :n], acc[:, n:]
+        ref = gt * torch.sigmoid(gt) * up
+    elif epi == "add":
+        res = torch.randn(m, n, generator=g).half()
+        ref = res.float() + acc
+    else:
+        ref = acc
+    xd = xbuf.to(dev)[:, 32:32 + k]
+    if epi == "add":
+        out = res.to(dev)
+        decode_gemm(xd, w.to(dev), out=out, epilogue="add")
+    else:
+        out = decode_gemm(xd, w.to(dev), epilogue=epi)
+    ok, err = rel_close(out.cpu(), ref, 4e-3, 2e-3)
+    assert ok, err
+
+
+def test_decode_gemm_rejects_unsupported_shapes(dev):
+    from mycustomcudaengine_amd import _lib
+    from mycustomcudaengine_amd.ops import decode_gemm
+    x = torch.zeros(17, 512, dtype=torch.float16, device=dev)
+    w = torch.zeros(64, 512, dtype=torch.float16, device=dev)
+    with pytest.raises(_lib.MCEError) as ei:
+        decode_gemm(x, w)
+    assert ei.value.code == _lib.MCE_ERR_UNSUPPORTED
