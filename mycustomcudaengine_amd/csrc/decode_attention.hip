@@ -42,11 +42,12 @@
 //     four whole 256-byte token rows (the pattern that streams fastest on
 //     MI355X; loading K in an MFMA-operand layout, 64-byte pieces of 16 rows
 //     per instruction, measured ~6% slower);
-//   * scores: v_dot2_f32_f16 over the lane's dims and a 16-lane DPP sum, so
-//     every lane of a group holds its tokens' scores for all G query heads;
+//   * scores: v_dot2_f32_f16 (v_dot2_f32_bf16 for bf16) over the lane's dims
+//     and a 16-lane DPP sum, so every lane of a group holds its tokens'
+//     scores for all G query heads;
 //   * online softmax in base 2 (p = exp2((s - m) c), c = scale log2 e);
-//   * P V with v_dot2_f32_f16 over token pairs, from the same registers --
-//     no LDS round trip for p.
+//   * P V with v_dot2 over token pairs (p packed as fp16 / bf16), from the
+//     same registers -- no LDS round trip for p.
 #include "mce_common.h"
 
 namespace mce {
@@ -68,7 +69,6 @@ constexpr int SEG_TILES = 1;
 // Context capacities up to this many tokens take the per-sequence mode.
 constexpr int PER_SEQ_MAX_TOKENS = 1024;
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 struct DecodeArgs {
   const uint16_t *query;    // [B, Hq, HD]
@@ -139,7 +139,7 @@ __device__ inline u32x4 ld_nt(const uint16_t *p) {
 
 // Two waves per SIMD: one 8-wave workgroup per CU.  (GQA groups of 7 or 8
 // query heads per kv head spill a few registers at this occupancy.)
-template <int G>
+template <class T, int G>
 __global__ __launch_bounds__(NT_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_kernel(DecodeArgs a) {
   const int hgrp = blockIdx.x, j = blockIdx.y;
@@ -232,7 +232,7 @@ void paged_decode_kernel(DecodeArgs a) {
     const int nparts = owner_of(pre[b + 1] - 1, NT, je) - j_first + 1;
 
     // This lane's slice of each query head: dims 8 lr .. 8 lr + 7 as packed
-    // fp16 pairs -- the same dims the lane loads from every K and V row.
+    // 16-bit pairs -- the same dims the lane loads from every K and V row.
     u32x4 qv[G];
 #pragma unroll
     for (int h = 0; h < G; ++h)
@@ -297,8 +297,7 @@ void paged_decode_kernel(DecodeArgs a) {
             for (int k = 0; k < 4; ++k)
               // (explicit conversions: bit_cast of an ext-vector element picks
               // element 0 in this compiler)
-              d = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, (uint32_t)kk[s8][k]),
-                                         __builtin_bit_cast(h2, (uint32_t)qv[h][k]), d, false);
+              d = T::dot2((uint32_t)kk[s8][k], (uint32_t)qv[h][k], d);
             d = row16_sum(d);
             sc[s8][h] = tv + s8 < t_end ? d : -INFINITY;
           }
@@ -340,23 +339,20 @@ void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int s8 = 0; s8 < 8; ++s8)
           if (tv + s8 >= t_end) vv[s8] = u32x4{0, 0, 0, 0};
-        // acc += P V over token pairs with v_dot2_f32_f16
+        // acc += P V over token pairs with v_dot2 (p packed in the element type)
 #pragma unroll
         for (int sp = 0; sp < 4; ++sp) {
-          h2 pp[G];
+          uint32_t pp[G];
 #pragma unroll
-          for (int h = 0; h < G; ++h)
-            pp[h] = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(p[2 * sp][h], p[2 * sp + 1][h]));
+          for (int h = 0; h < G; ++h) pp[h] = T::pack_p(p[2 * sp][h], p[2 * sp + 1][h]);
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
-            const h2 lo = __builtin_bit_cast(
-                h2, __builtin_amdgcn_perm(vv[2 * sp + 1][k], vv[2 * sp][k], 0x05040100u));
-            const h2 hi = __builtin_bit_cast(
-                h2, __builtin_amdgcn_perm(vv[2 * sp + 1][k], vv[2 * sp][k], 0x07060302u));
+            const uint32_t lo = __builtin_amdgcn_perm(vv[2 * sp + 1][k], vv[2 * sp][k], 0x05040100u);
+            const uint32_t hi = __builtin_amdgcn_perm(vv[2 * sp + 1][k], vv[2 * sp][k], 0x07060302u);
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-              acc[h][2 * k] = __builtin_amdgcn_fdot2(lo, pp[h], acc[h][2 * k], false);
-              acc[h][2 * k + 1] = __builtin_amdgcn_fdot2(hi, pp[h], acc[h][2 * k + 1], false);
+              acc[h][2 * k] = T::dot2(lo, pp[h], acc[h][2 * k]);
+              acc[h][2 * k + 1] = T::dot2(hi, pp[h], acc[h][2 * k + 1]);
             }
           }
         }
@@ -409,7 +405,7 @@ void paged_decode_kernel(DecodeArgs a) {
             u32x4 o;
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-              o[k] = pack2<F16T>(acc[h][2 * k] * inv, acc[h][2 * k + 1] * inv);
+              o[k] = pack2<T>(acc[h][2 * k] * inv, acc[h][2 * k + 1] * inv);
             *reinterpret_cast<u32x4 *>(a.out + (row0 + h) * HD + lr * 8) = o;
           } else {
             const int64_t pr = (row0 + h) * a.J + slot;
@@ -460,7 +456,7 @@ void paged_decode_kernel(DecodeArgs a) {
       }
       const int64_t row = (int64_t)b * a.Hq + (hgrp * hpg + hh) * G + h;
       if (nparts == 1) {
-        a.out[row * HD + d] = F16T::from_float(A / L);
+        a.out[row * HD + d] = T::from_float(A / L);
       } else {
         const int64_t pr = row * a.J + slot;
         a.ws_acc[pr * HD + d] = A;
@@ -478,6 +474,7 @@ void paged_decode_kernel(DecodeArgs a) {
 // a time: lane i loads part i's (m, l), the block max rescales them into LDS
 // weights, and every lane then streams its dim of the partial outputs with
 // independent (unrolled) loads.
+template <class T>
 __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int64_t row = (int64_t)b * a.Hq + h;
@@ -533,7 +530,7 @@ __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
     M = m_new;
     lds_barrier();
   }
-  a.out[row * HD + d] = F16T::from_float(A / L);
+  a.out[row * HD + d] = T::from_float(A / L);
 }
 
 struct DecodeLayout {
@@ -580,9 +577,6 @@ extern "C" int mce_paged_attention_decode(
   clear_error();
   MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16,
               "mce_paged_attention_decode: unknown dtype %d", dtype);
-  if (dtype != MCE_F16)
-    return set_error(MCE_ERR_UNSUPPORTED,
-                     "mce_paged_attention_decode: only fp16 is implemented");
   MCE_REQUIRE(head_dim == HD, "mce_paged_attention_decode: head_dim must be 128 (got %d)", head_dim);
   MCE_REQUIRE(batch >= 0 && num_heads >= 1 && num_kv_heads >= 1,
               "mce_paged_attention_decode: bad head counts");
@@ -654,21 +648,28 @@ extern "C" int mce_paged_attention_decode(
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid = per_seq ? dim3(num_kv_heads, batch) : dim3(Lay.groups, Lay.J);
-#define MCE_DEC_CASE(GG)                                                       \
+#define MCE_DEC_CASE(TT, GG)                                                   \
   case GG:                                                                     \
-    paged_decode_kernel<GG><<<grid, NT_THREADS, 0, st>>>(a);                   \
+    paged_decode_kernel<TT, GG><<<grid, NT_THREADS, 0, st>>>(a);               \
     break;
-  switch (G) {
-    MCE_DEC_CASE(1)
-    MCE_DEC_CASE(2)
-    MCE_DEC_CASE(3)
-    MCE_DEC_CASE(4)
-    MCE_DEC_CASE(5)
-    MCE_DEC_CASE(6)
-    MCE_DEC_CASE(7)
-    MCE_DEC_CASE(8)
+#define MCE_DEC_LAUNCH(TT)                                                     \
+  switch (G) {                                                                 \
+    MCE_DEC_CASE(TT, 1)                                                        \
+    MCE_DEC_CASE(TT, 2)                                                        \
+    MCE_DEC_CASE(TT, 3)                                                        \
+    MCE_DEC_CASE(TT, 4)                                                        \
+    MCE_DEC_CASE(TT, 5)                                                        \
+    MCE_DEC_CASE(TT, 6)                                                        \
+    MCE_DEC_CASE(TT, 7)                                                        \
+    MCE_DEC_CASE(TT, 8)                                                        \
+  }                                                                            \
+  if (!per_seq) paged_decode_merge_kernel<TT><<<dim3(num_heads, batch), HD, 0, st>>>(a);
+  if (dtype == MCE_F16) {
+    MCE_DEC_LAUNCH(F16T)
+  } else {
+    MCE_DEC_LAUNCH(BF16T)
   }
+#undef MCE_DEC_LAUNCH
 #undef MCE_DEC_CASE
-  if (!per_seq) paged_decode_merge_kernel<<<dim3(num_heads, batch), HD, 0, st>>>(a);
   return check_launch("mce_paged_attention_decode");
 }

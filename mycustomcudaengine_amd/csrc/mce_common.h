@@ -51,6 +51,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 // Storage-type traits: conversion of 16-bit storage values to/from fp32.
 struct F16T {
@@ -63,6 +66,15 @@ struct F16T {
   }
   __device__ static inline uint16_t from_float(float x) {
     return __builtin_bit_cast(uint16_t, (f16)x);
+  }
+  // c + a.lo * b.lo + a.hi * b.hi over packed pairs (v_dot2_f32_f16)
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a), __builtin_bit_cast(f16x2, b), c,
+                                  false);
+  }
+  // two probabilities as a packed operand (v_cvt_pkrtz_f16_f32)
+  __device__ static inline uint32_t pack_p(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
   }
 };
 
@@ -80,6 +92,16 @@ struct BF16T {
     if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
     u += 0x7fffu + ((u >> 16) & 1u);
     return (uint16_t)(u >> 16);
+  }
+  // c + a.lo * b.lo + a.hi * b.hi over packed pairs (v_dot2_f32_bf16)
+  __device__ static inline float dot2(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
+                                           __builtin_bit_cast(bf16x2, b), c, false);
+  }
+  // two probabilities as a packed operand (v_cvt_pk_bf16_f32, nearest even)
+  __device__ static inline uint32_t pack_p(float a, float b) {
+    const bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, v);
   }
 };
 

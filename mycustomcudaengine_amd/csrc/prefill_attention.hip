@@ -50,7 +50,16 @@ constexpr float RESCALE_TAU = 8.0f;  // log2 headroom before raising the max
 // parts: data format 32, no swizzle, range-checked against num_records.
 constexpr int BUF_RSRC_WORD3 = 0x00020000;
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+// v_mfma_f32_32x32x16 on raw 16-bit operands of the element type.
+template <class T>
+__device__ __forceinline__ floatx16 mfma32(u32x4 a, u32x4 b, floatx16 c) {
+  if constexpr (T::code == MCE_F16)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, a),
+                                                  __builtin_bit_cast(half8, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
 
 // Position of key offset o (0..31) within a V^T row: bits 2 and 3 swapped,
 // so the 8 keys one lane feeds to a P V MFMA (4 hf + 0..3 and 8 + 4 hf + 0..3
@@ -98,7 +107,7 @@ struct PrefillArgs {
 // halved; the streams keep separate online-softmax states that are merged
 // through LDS at the end.  KSPLIT = 1 suits grids with several workgroups
 // per CU, where the co-resident workgroups already fill the SIMDs.
-template <int NRB, int KSPLIT>
+template <class T, int NRB, int KSPLIT>
 __global__ __launch_bounds__(NRB * KSPLIT * 64) __attribute__((amdgpu_waves_per_eu(PF_WAVES_PER_EU, PF_WAVES_PER_EU)))
 void prefill_causal_kernel(PrefillArgs a) {
   constexpr int BM = 32 * NRB;
@@ -227,19 +236,27 @@ void prefill_causal_kernel(PrefillArgs a) {
   const int n_full = min((wave_min_pos + 1) / PF_BN, S / PF_BN);
   const int lim = min(pos, S - 1) - 4 * hf;  // masked tiles: key offset limit + n0
 
-  // Q^T as MFMA B operand, pre-scaled by c: lane supplies
-  // c Q[pos, h][16 i + 8 hf + j].
-  half8 qreg[8];
+  // Q^T as MFMA B operand: lane supplies Q[pos, h][16 i + 8 hf + j], for fp16
+  // pre-scaled by c (so the accumulators come out in log2 units); bf16 keeps
+  // Q exact (its 8-bit mantissa would round c Q too coarsely) and scales the
+  // scores instead (PRESCALED false).
+  constexpr bool PRESCALED = T::code == MCE_F16;
+  u32x4 qreg[8];
   {
     const uint16_t *qp = a.q + ((int64_t)b * S + (row_ok ? pos : 0)) * q_row_stride +
                          (int64_t)(row_ok ? h : 0) * PF_HD + 8 * hf;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const half8 x = row_ok ? __builtin_bit_cast(
-                                   half8, *reinterpret_cast<const u32x4 *>(qp + 16 * i))
-                             : half8{0, 0, 0, 0, 0, 0, 0, 0};
+      const u32x4 x = row_ok ? *reinterpret_cast<const u32x4 *>(qp + 16 * i) : u32x4{0, 0, 0, 0};
+      if constexpr (PRESCALED) {
+        const half8 xh = __builtin_bit_cast(half8, x);
+        half8 y;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) qreg[i][j] = (_Float16)((float)x[j] * c);
+        for (int j = 0; j < 8; ++j) y[j] = (_Float16)((float)xh[j] * c);
+        qreg[i] = __builtin_bit_cast(u32x4, y);
+      } else {
+        qreg[i] = x;
+      }
     }
   }
 
@@ -249,10 +266,8 @@ void prefill_causal_kernel(PrefillArgs a) {
     for (int e = 0; e < 16; ++e) st[e] = init;
     const uint16_t *kp = &ks[r32 * KS_PITCH + 8 * hf];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      half8 ka = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4 *>(kp + 16 * i));
-      st = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, qreg[i], st, 0, 0, 0);
-    }
+    for (int i = 0; i < 8; ++i)
+      st = mfma32<T>(*reinterpret_cast<const u32x4 *>(kp + 16 * i), qreg[i], st);
   };
 
   // Running max m_run (scaled units) is 0 until the row has seen an unmasked
@@ -265,7 +280,7 @@ void prefill_causal_kernel(PrefillArgs a) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
   floatx16 s_a, s_b;  // scores of the current / next tile, ping-ponged
-  const h2 ones = {(_Float16)1.0f, (_Float16)1.0f};
+  const uint32_t ones = T::pack_p(1.0f, 1.0f);
 
   // Prologue (per key stream): K_0 staged and scored; K_1 and V_0 staged into
   // the second / first buffers; (K_2, V_1) fetched into register set 0 and
@@ -295,6 +310,10 @@ void prefill_causal_kernel(PrefillArgs a) {
     lds_barrier();
     const int kt = KSPLIT * u + kh;  // key tile
     if (kt < n_wtiles) {
+      if constexpr (!PRESCALED) {  // raw scores -> log2 units, relative to m
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s_cur[e] = __builtin_fmaf(s_cur[e], c, -m_run);
+      }
       if (kt >= n_full) {  // diagonal / end-of-sequence tile
         const int l2 = lim - kt * PF_BN;
 #pragma unroll
@@ -328,11 +347,11 @@ void prefill_causal_kernel(PrefillArgs a) {
       // MFMAs and the exp work instead of stalling each MFMA in turn.
       const uint16_t *kp = &ks_h[((u + 1) & 1) * KS_SIZE + r32 * KS_PITCH + 8 * hf];
       const uint16_t *vp = &vt_h[(u & 1) * VT_SIZE + r32 * VT_PITCH + 8 * hf];
-      half8 kf[8];
+      u32x4 kf[8];
       u32x4 vf[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        kf[i] = __builtin_bit_cast(half8, *reinterpret_cast<const u32x4 *>(kp + 16 * i));
+        kf[i] = *reinterpret_cast<const u32x4 *>(kp + 16 * i);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -341,26 +360,23 @@ void prefill_causal_kernel(PrefillArgs a) {
               *reinterpret_cast<const u32x4 *>(vp + dt * 32 * VT_PITCH + 16 * kk);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s_nxt[e] = -m_run;
+      for (int e = 0; e < 16; ++e) s_nxt[e] = PRESCALED ? -m_run : 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        s_nxt = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[i], qreg[i], s_nxt, 0, 0, 0);
-      half8 pk[2];
+      for (int i = 0; i < 8; ++i) s_nxt = mfma32<T>(kf[i], qreg[i], s_nxt);
+      u32x4 pk[2];
 #pragma unroll
       for (int e2 = 0; e2 < 8; ++e2) {
         const float p0 = fast_exp2(s_cur[2 * e2]);
         const float p1 = fast_exp2(s_cur[2 * e2 + 1]);
-        const h2 pp = __builtin_bit_cast(h2, __builtin_amdgcn_cvt_pkrtz(p0, p1));
-        l_i = __builtin_amdgcn_fdot2(pp, ones, l_i, false);
-        pk[e2 >> 2][2 * (e2 & 3)] = pp[0];
-        pk[e2 >> 2][2 * (e2 & 3) + 1] = pp[1];
+        const uint32_t pp = T::pack_p(p0, p1);
+        l_i = T::dot2(pp, ones, l_i);
+        pk[e2 >> 2][e2 & 3] = pp;
       }
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, vf[dt * 2 + kk]),
-                                                         pk[kk], o[dt], 0, 0, 0);
+          o[dt] = mfma32<T>(vf[dt * 2 + kk], pk[kk], o[dt]);
       PF_SCHEDULE();
     }
     // stage K_{u+2} into buffer u%2 (read as K_u in iteration u-1) and
@@ -425,8 +441,8 @@ void prefill_causal_kernel(PrefillArgs a) {
           if constexpr (KSPLIT == 2) v[j] += xo[(dt * 16 + e) * 64] * s1;
         }
         u32x2 pr;
-        pr[0] = pack2<F16T>(v[0], v[1]);
-        pr[1] = pack2<F16T>(v[2], v[3]);
+        pr[0] = pack2<T>(v[0], v[1]);
+        pr[1] = pack2<T>(v[2], v[3]);
         *reinterpret_cast<u32x2 *>(op + dt * 32 + 8 * e4) = pr;
       }
   }
@@ -444,9 +460,6 @@ extern "C" int mce_prefill_attention(int dtype, const void *query,
   clear_error();
   MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16,
               "mce_prefill_attention: unknown dtype %d", dtype);
-  if (dtype != MCE_F16)
-    return set_error(MCE_ERR_UNSUPPORTED,
-                     "mce_prefill_attention: only fp16 is implemented");
   MCE_REQUIRE(head_dim == PF_HD,
               "mce_prefill_attention: head_dim must be 128 (got %d)", head_dim);
   MCE_REQUIRE(batch >= 0 && seq_len >= 0 && num_heads >= 1 && num_kv_heads >= 1,
@@ -486,9 +499,17 @@ extern "C" int mce_prefill_attention(int dtype, const void *query,
   const int64_t grid = (int64_t)a.n_items * batch * num_kv_heads;
   MCE_REQUIRE(grid < ((int64_t)1 << 31), "mce_prefill_attention: problem too large");
   hipStream_t st = (hipStream_t)stream;
-  if (grid < 2 * (int64_t)cu_count())
-    prefill_causal_kernel<nrb, 2><<<(unsigned)grid, nrb * 128, 0, st>>>(a);
-  else
-    prefill_causal_kernel<nrb, 1><<<(unsigned)grid, nrb * 64, 0, st>>>(a);
+  const bool split = grid < 2 * (int64_t)cu_count();
+  if (dtype == MCE_F16) {
+    if (split)
+      prefill_causal_kernel<F16T, nrb, 2><<<(unsigned)grid, nrb * 128, 0, st>>>(a);
+    else
+      prefill_causal_kernel<F16T, nrb, 1><<<(unsigned)grid, nrb * 64, 0, st>>>(a);
+  } else {
+    if (split)
+      prefill_causal_kernel<BF16T, nrb, 2><<<(unsigned)grid, nrb * 128, 0, st>>>(a);
+    else
+      prefill_causal_kernel<BF16T, nrb, 1><<<(unsigned)grid, nrb * 64, 0, st>>>(a);
+  }
   return check_launch("mce_prefill_attention");
 }

@@ -86,7 +86,7 @@ def test_decode_validation(lib):
     assert _decode(lib, bs=12) == _lib.MCE_ERR_INVALID and "block_size" in _err(lib)
     assert _decode(lib, bs=4) == _lib.MCE_ERR_INVALID
     assert _decode(lib, Hq=80) == _lib.MCE_ERR_UNSUPPORTED  # GQA group 10
-    assert _decode(lib, dtype=1) == _lib.MCE_ERR_UNSUPPORTED
+    assert _decode(lib, dtype=1) == _lib.MCE_ERR_WORKSPACE  # bf16 is supported
     assert _decode(lib, q=None) == _lib.MCE_ERR_INVALID
     assert _decode(lib, nb=0) == _lib.MCE_ERR_INVALID
     assert _decode(lib) == _lib.MCE_ERR_WORKSPACE  # no workspace given

@@ -30,7 +30,7 @@ def check(case, dev, tol=TOL):
     out = run_gpu(case, dev)
     ref = decode_attention_ref(case.query, case.key_cache, case.value_cache,
                                case.block_tables, case.context_lens, case.scale)
-    assert out.shape == ref.shape and out.dtype == torch.float16
+    assert out.shape == ref.shape and out.dtype == case.query.dtype
     assert not torch.isnan(out).any(), "NaN in output (pool sentinel leaked?)"
     err = (out.float() - ref).abs().max().item()
     assert err <= tol, f"max abs err {err}"
@@ -145,9 +145,19 @@ def test_rejects_bad_inputs(dev):
                                    case.scale)
 
 
+@pytest.mark.parametrize("ctxs,mb", [([512], None), ([3000, 129, 2048, 4096], None),
+                                     ([600] * 8, 48), ([9000, 700], 1024), ([0, 33, 1], 4)])
+def test_bf16(dev, ctxs, mb):
+    """bf16 caches and query (v_dot2_f32_bf16 scores and P V, p packed as
+    bf16): split-K and per-sequence modes, empty and one-token rows."""
+    case = make_decode_case(50 + len(ctxs) + sum(ctxs) % 7, len(ctxs), ctxs, max_blocks=mb,
+                            dtype=torch.bfloat16)
+    check(case, dev)
+
+
 def test_workspace_reuse_across_shapes(dev):
-    """The split-K arrival counters live in a reused workspace and must be left
-    at zero by every call: alternate multi-chunk shapes and re-check each."""
+    """Alternate multi-part shapes through fresh workspaces and re-check each
+    (partials of one call never leak into the next)."""
     cases = [make_decode_case(40, 4, [3000, 129, 2048, 4096]),
              make_decode_case(41, 2, [9000, 700], max_blocks=1024),
              make_decode_case(42, 8, [600] * 8)]

@@ -176,6 +176,20 @@ def test_prefill_matches_oracle(dev, s, hq, hkv):
     assert err <= TOL, err
 
 
+@pytest.mark.parametrize("b,s,hq,hkv", [(1, 300, 24, 8), (2, 129, 6, 2), (1, 1, 4, 4),
+                                         (8, 512, 24, 8)])
+def test_prefill_bf16_matches_oracle(dev, b, s, hq, hkv):
+    """bf16 Q/K/V (bf16 MFMA, exact Q, scores scaled in fp32, P as bf16) on
+    both kernel shapes (the last case is a large grid)."""
+    case = make_prefill_case(90 + s, b, s, hq, hkv, dtype=torch.bfloat16)
+    out = ops.prefill_attention(case.query.to(dev), case.key.to(dev), case.value.to(dev),
+                                case.scale).cpu()
+    assert out.dtype == torch.bfloat16 and not torch.isnan(out).any()
+    ref = prefill_attention_ref(case.query, case.key, case.value, case.scale)
+    err = (out.float() - ref).abs().max().item()
+    assert err <= TOL, err
+
+
 @pytest.mark.parametrize("b,s", [(8, 512), (6, 700)])
 def test_prefill_large_grid_matches_oracle(dev, b, s):
     """Grids of at least two workgroups per CU take the kernel without the
