@@ -19,10 +19,12 @@
 //     from the S^T registers, converted to f16): lane l again holds row
 //     (l % 32), so the online-softmax rescale is a per-lane multiply.
 // The k-index permutation used for P^T (keys 8(v/4) + 4(l/32) + v%4 of the
-// S^T output layout) is mirrored by the V^T reads: V is transposed into LDS
-// ([dim][key], keys of each 16-key group stored in the order the fragments
-// consume them) on the way in, so every MFMA operand is one 16-byte LDS read;
-// K is stored row-major with a 16-byte row pad (conflict-free 16-byte reads).
+// S^T output layout) is mirrored by the V^T operand reads: V is staged
+// row-major like K and read with the transposing ds_read_b64_tr_b16, two per
+// fragment (keys 4(l/32) + 0..3 and 8 + 4(l/32) + 0..3 of a 16-key group), so
+// no transpose runs on the VALU.  K rows are padded by 16 bytes (272-byte
+// pitch: conflict-free 16-byte fragment reads), V rows by 64 bytes (320-byte
+// pitch: each transposing read touches 8 rows x 64 bytes, two per bank).
 //
 // Software pipeline: the scores of key tile k+1 are computed in the same
 // straight-line block as the softmax and P V of tile k, so the exp/convert
@@ -39,12 +41,14 @@
 // same f16 P values that enter P V.
 #include "mce_common.h"
 
+#include <type_traits>
+
 namespace mce {
 
 constexpr int PF_HD = 128;
 constexpr int PF_BN = 32;
 constexpr int KS_PITCH = PF_HD + 8;  // halfs per K row in LDS (272 B)
-constexpr int VT_PITCH = PF_BN + 8;  // halfs per V^T row in LDS (80 B)
+constexpr int VS_PITCH = PF_HD + 32;  // halfs per V row in LDS (320 B)
 constexpr float RESCALE_TAU = 8.0f;  // log2 headroom before raising the max
 // Buffer descriptor word 3 for raw (stride 0) dword loads on gfx9-family
 // parts: data format 32, no swizzle, range-checked against num_records.
@@ -61,13 +65,14 @@ __device__ __forceinline__ floatx16 mfma32(u32x4 a, u32x4 b, floatx16 c) {
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// Position of key offset o (0..31) within a V^T row: bits 2 and 3 swapped,
-// so the 8 keys one lane feeds to a P V MFMA (4 hf + 0..3 and 8 + 4 hf + 0..3
-// of a 16-key group) sit in 16 contiguous bytes: one ds_read_b128 per
-// fragment.  The 80-byte row pitch keeps those reads conflict-free (16 rows
-// step through 16 distinct 4-bank groups).
-__device__ __forceinline__ int vt_pos(int o) {
-  return (o & ~12) | ((o & 4) << 1) | ((o & 8) >> 1);
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane s supplies the address
+// of 4 consecutive 16-bit values (row s / 4, columns 4 (s % 4) .. +3 of a
+// 4 x 16 block) and lane d receives column d of the block's 4 rows.
+__device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t *p) {
+  return __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)p));
 }
 
 // max(x[l], x[l ^ 32]) in every lane: v_permlane32_swap exchanges the two
@@ -113,16 +118,14 @@ void prefill_causal_kernel(PrefillArgs a) {
   constexpr int BM = 32 * NRB;
   constexpr int NT = NRB * 64;                     // threads per key stream
   constexpr int K_PIECES = PF_BN * PF_HD / 8;      // 16-byte pieces per K tile
-  constexpr int V_GROUPS = PF_BN / 2 * PF_HD / 8;  // 2-key x 8-dim groups per V tile
-  constexpr int KP = K_PIECES / NT;
-  constexpr int VG = V_GROUPS / NT;
-  static_assert(KP * NT == K_PIECES && VG * NT == V_GROUPS, "whole tiles per thread");
-  constexpr int KS_SIZE = PF_BN * KS_PITCH, VT_SIZE = PF_HD * VT_PITCH;
-  // [key stream][double buffer] K and V^T tiles; reused for the final merge
-  constexpr int LDS_HALFS = 2 * KSPLIT * (KS_SIZE + VT_SIZE);
+  constexpr int KP = K_PIECES / NT;               // per thread, K and V alike
+  static_assert(KP * NT == K_PIECES, "whole tiles per thread");
+  constexpr int KS_SIZE = PF_BN * KS_PITCH, VS_SIZE = PF_BN * VS_PITCH;
+  // [key stream][double buffer] K and V tiles; reused for the final merge
+  constexpr int LDS_HALFS = 2 * KSPLIT * (KS_SIZE + VS_SIZE);
   __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALFS];
   uint16_t *const Ks = lds;
-  uint16_t *const Vt = lds + 2 * KSPLIT * KS_SIZE;
+  uint16_t *const Vs = lds + 2 * KSPLIT * KS_SIZE;
 
   // workgroup -> (item, batch, kv head); kv head fastest so that the
   // workgroups of one kv head share an XCD (and its L2) when Hkv B == 8.
@@ -138,7 +141,7 @@ void prefill_causal_kernel(PrefillArgs a) {
   const int tid_h = tid - kh * NT;  // thread index within the key stream
   const int hf = lane >> 5, r32 = lane & 31;
   uint16_t *const ks_h = Ks + kh * 2 * KS_SIZE;
-  uint16_t *const vt_h = Vt + kh * 2 * VT_SIZE;
+  uint16_t *const vs_h = Vs + kh * 2 * VS_SIZE;
 
   const int64_t q_row_stride = (int64_t)a.Hq * PF_HD;
   const int kv_row = a.Hkv * PF_HD;  // elements between consecutive keys
@@ -146,11 +149,9 @@ void prefill_causal_kernel(PrefillArgs a) {
   const uint16_t *vbase = a.v + ((int64_t)b * S * a.Hkv + g) * PF_HD;
   const float c = a.scale_log2;
 
-  // Per-thread staging assignments within a key stream (fixed for the kernel).
-  //  K: piece pc -> key pc / 16, 16-byte column pc % 16 (16 lanes per key row).
-  //  V: group gc -> keys 2 (gc % 16) .. +1, dims 8 (gc / 16) .. +7: after a
-  //     2-key x 8-dim transpose in registers, 16 lanes write one V^T row run.
-  // Two register sets: a tile is fetched two iterations before it is staged.
+  // Per-thread staging assignments within a key stream (fixed for the kernel):
+  // piece pc -> key pc / 16, 16-byte column pc % 16 (16 lanes per key row),
+  // the same for K and V.  Two register sets: a tile is fetched two iterations before it is staged.
   // Loads are unconditional buffer loads (straight-line code keeps the
   // compiler's vmcnt accounting exact, so staging waits only for the set it
   // stores) with loop-invariant per-thread offsets; the hardware range check
@@ -161,58 +162,47 @@ void prefill_causal_kernel(PrefillArgs a) {
       __builtin_amdgcn_make_buffer_rsrc((void *)kbase, (short)0, kv_bytes, BUF_RSRC_WORD3);
   const __amdgpu_buffer_rsrc_t vrsrc =
       __builtin_amdgcn_make_buffer_rsrc((void *)vbase, (short)0, kv_bytes, BUF_RSRC_WORD3);
-  int k_voff[KP], v_voff[VG * 2];
+  int kv_voff[KP];
 #pragma unroll
   for (int it = 0; it < KP; ++it) {
     const int pc = tid_h + it * NT;
-    k_voff[it] = ((pc >> 4) * kv_row + (pc & 15) * 8) * 2;
+    kv_voff[it] = ((pc >> 4) * kv_row + (pc & 15) * 8) * 2;
   }
-#pragma unroll
-  for (int gi = 0; gi < VG; ++gi)
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int gc = tid_h + gi * NT;
-      v_voff[gi * 2 + kk] = ((2 * (gc & 15) + kk) * kv_row + (gc >> 4) * 8) * 2;
-    }
   // stream index u of this key stream <-> key tile KSPLIT u + kh
-  auto tile_off = [&](int u) { return (KSPLIT * u + kh) * PF_BN * kv_row * 2; };
-  u32x4 kreg[2][KP], vreg[2][VG * 2];
-  auto load_k = [&](int set, int u) {
+  // (wave-uniform, passed as the scalar offset of the buffer loads)
+  auto tile_off = [&](int u) {
+    return __builtin_amdgcn_readfirstlane((KSPLIT * u + kh) * PF_BN * kv_row * 2);
+  };
+  using KRegs = u32x4[KP];
+  using VRegs = u32x4[KP];
+  KRegs kreg[2];
+  VRegs vreg[2];
+  auto load_k = [&](KRegs &dst, int u) {
     const int off = tile_off(u);
 #pragma unroll
     for (int it = 0; it < KP; ++it)
-      kreg[set][it] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krsrc, k_voff[it] + off, 0, 0));
+      dst[it] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krsrc, kv_voff[it], off, 0));
   };
-  auto load_v = [&](int set, int u) {
+  auto load_v = [&](VRegs &dst, int u) {
     const int off = tile_off(u);
 #pragma unroll
-    for (int j = 0; j < VG * 2; ++j)
-      vreg[set][j] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrsrc, v_voff[j] + off, 0, 0));
+    for (int it = 0; it < KP; ++it)
+      dst[it] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrsrc, kv_voff[it], off, 0));
   };
-  auto store_k = [&](int set, uint16_t *ks) {
+  auto store_k = [&](const KRegs &src, uint16_t *ks) {
 #pragma unroll
     for (int it = 0; it < KP; ++it) {
       const int pc = tid_h + it * NT;
-      *reinterpret_cast<u32x4 *>(&ks[(pc >> 4) * KS_PITCH + (pc & 15) * 8]) = kreg[set][it];
+      *reinterpret_cast<u32x4 *>(&ks[(pc >> 4) * KS_PITCH + (pc & 15) * 8]) = src[it];
     }
   };
-  auto store_v = [&](int set, uint16_t *vt) {
+  auto store_v = [&](const VRegs &src, uint16_t *vs) {
 #pragma unroll
-    for (int gi = 0; gi < VG; ++gi) {
-      const int gc = tid_h + gi * NT;
-      const int key0 = 2 * (gc & 15), piece = gc >> 4;
-      const u32x4 *x = &vreg[set][gi * 2];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // dims 8 piece + 2e (low halves) and + 2e + 1 (high halves)
-        const int d = piece * 8 + 2 * e;
-        *reinterpret_cast<uint32_t *>(&vt[d * VT_PITCH + vt_pos(key0)]) =
-            __builtin_amdgcn_perm(x[1][e], x[0][e], 0x05040100u);
-        *reinterpret_cast<uint32_t *>(&vt[(d + 1) * VT_PITCH + vt_pos(key0)]) =
-            __builtin_amdgcn_perm(x[1][e], x[0][e], 0x07060302u);
-      }
+    for (int it = 0; it < KP; ++it) {
+      const int pc = tid_h + it * NT;
+      *reinterpret_cast<u32x4 *>(&vs[(pc >> 4) * VS_PITCH + (pc & 15) * 8]) = src[it];
     }
   };
 
@@ -241,22 +231,34 @@ void prefill_causal_kernel(PrefillArgs a) {
   // Q exact (its 8-bit mantissa would round c Q too coarsely) and scales the
   // scores instead (PRESCALED false).
   constexpr bool PRESCALED = T::code == MCE_F16;
+  //
+  // Q, K_0, K_1 and V_0 are fetched together (one memory round trip before
+  // the first tile instead of one per dependent stage); the two register
+  // sets follow once K_0 is staged.
   u32x4 qreg[8];
   {
     const uint16_t *qp = a.q + ((int64_t)b * S + (row_ok ? pos : 0)) * q_row_stride +
                          (int64_t)(row_ok ? h : 0) * PF_HD + 8 * hf;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const u32x4 x = row_ok ? *reinterpret_cast<const u32x4 *>(qp + 16 * i) : u32x4{0, 0, 0, 0};
-      if constexpr (PRESCALED) {
-        const half8 xh = __builtin_bit_cast(half8, x);
-        half8 y;
+    for (int i = 0; i < 8; ++i) qreg[i] = *reinterpret_cast<const u32x4 *>(qp + 16 * i);
+  }
+  KRegs k0, k1;
+  VRegs v0;
+  load_k(k0, 0);
+  load_k(k1, 1);
+  load_v(v0, 0);
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) y[j] = (_Float16)((float)xh[j] * c);
-        qreg[i] = __builtin_bit_cast(u32x4, y);
-      } else {
-        qreg[i] = x;
-      }
+  for (int i = 0; i < 8; ++i) {
+    const u32x4 x = row_ok ? qreg[i] : u32x4{0, 0, 0, 0};
+    if constexpr (PRESCALED) {
+      const half8 xh = __builtin_bit_cast(half8, x);
+      half8 y;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) y[j] = (_Float16)((float)xh[j] * c);
+      qreg[i] = __builtin_bit_cast(u32x4, y);
+    } else {
+      qreg[i] = x;
     }
   }
 
@@ -270,132 +272,201 @@ void prefill_causal_kernel(PrefillArgs a) {
       st = mfma32<T>(*reinterpret_cast<const u32x4 *>(kp + 16 * i), qreg[i], st);
   };
 
-  // Running max m_run (scaled units) is 0 until the row has seen an unmasked
-  // key (m_set); l_i is this lane's half of the row sum.
-  float m_run = 0.f, l_i = 0.f;
-  bool m_set = false;
+  // Online-softmax state of this lane's row: running max m_run (log2 units;
+  // 0 until the row has seen an unmasked key), growth threshold thr (-inf
+  // until then, so the first finite tile max sets m_run; RESCALE_TAU after),
+  // l_i = this lane's half of the row sum, O^T in o.
+  float m_run = 0.f, thr = -INFINITY, l_i = 0.f;
   floatx16 o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
-  floatx16 s_a, s_b;  // scores of the current / next tile, ping-ponged
+  floatx16 s_a, s_b;  // ping-pong: scores ready for exp / next accumulator
+  // accumulator start of every tile's scores: -m_run (fp16, pre-scaled Q) or 0
+  floatx16 acc0;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc0[e] = 0.f;
   const uint32_t ones = T::pack_p(1.0f, 1.0f);
 
-  // Prologue (per key stream): K_0 staged and scored; K_1 and V_0 staged into
-  // the second / first buffers; (K_2, V_1) fetched into register set 0 and
-  // (K_3, V_2) into set 1 (indices are stream indices u).
-  load_k(0, 0);
-  store_k(0, ks_h);
-  load_k(0, 1);
-  load_v(0, 0);
-  lds_barrier();
-  if (kh < n_wtiles) scores(ks_h, 0.f, s_a);
-  store_k(0, ks_h + KS_SIZE);
-  store_v(0, vt_h);
-  load_k(0, 2);
-  load_v(0, 1);
-  load_k(1, 3);
-  load_v(1, 2);
+  // Scores of key tile kt straight from the MFMA -> exp2 arguments: bf16
+  // scales them here; tiles past the diagonal (or the sequence end) get -inf
+  // on masked keys.
+  auto prep = [&](floatx16 &s, const int kt) {
+    if constexpr (!PRESCALED) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[e] = __builtin_fmaf(s[e], c, -m_run);
+    }
+    if (kt >= n_full) {
+      const int l2 = lim - kt * PF_BN;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (8 * (e >> 2) + (e & 3) > l2) s[e] = -INFINITY;
+    }
+  };
+  // max over this lane's row (both halves)
+  auto rowmax = [&](const floatx16 &s) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[e]);
+    return fmaxf(mx, xor32_max(mx));
+  };
+  // Raise the running max of the rows whose tile max exceeds thr: O, l and
+  // the ready scores move to the new max.  Rare after the first tile (growth
+  // beyond 2^TAU in p units).
+  auto rescale = [&](const float mx, floatx16 &s_ready) {
+    const bool grow = mx > thr;
+    const float d = grow ? mx : 0.f;
+    const float alpha = thr > -INFINITY ? fast_exp2(-d) : 0.f;
+    l_i *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s_ready[e] -= d;
+    m_run += d;
+    if constexpr (PRESCALED) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc0[e] = -m_run;
+    }
+    thr = grow ? RESCALE_TAU : thr;
+  };
 
-  // Iteration u: softmax + P V of tile u (scores already in s_cur), scores of
-  // tile u + 1 (K in buffer (u+1)%2), then stage K_{u+2} / V_{u+1} from
-  // register set u%2 into the buffers that iteration u - 1 finished reading
-  // and fetch K_{u+4} / V_{u+3} into that set.  Barriers match by count:
+  // Prologue (per key stream): K_0 staged and scored (prepared in s_a); K_1
+  // and V_0 staged into the second
+  // / first buffers; (K_2, V_1) fetched into register set 0, then (K_3, V_2)
+  // into set 1, so each staging step below waits only for the older set
+  // (indices are stream indices u).
+  store_k(k0, ks_h);
+  lds_barrier();
+  load_k(kreg[0], 2);
+  load_v(vreg[0], 1);
+  __builtin_amdgcn_sched_barrier(0);
+  load_k(kreg[1], 3);
+  load_v(vreg[1], 2);
+  __builtin_amdgcn_sched_barrier(0);
+  {
+    scores(ks_h, 0.f, s_a);
+    prep(s_a, kh);
+    const float mx = rowmax(s_a);
+    if (__ballot(mx > thr) != 0) rescale(mx, s_a);
+  }
+  store_k(k1, ks_h + KS_SIZE);
+  store_v(v0, vs_h);
+
+  // Iteration u (key tile kt = KSPLIT u + kh), one straight-line block:
+  //   A: scores of tile u + 1 (K in buffer (u+1)%2, accumulators starting at
+  //      -m_run) on the matrix cores while the exp2 / convert / row-sum work
+  //      of tile u runs on the VALU;
+  //   K_{u+2} / V_{u+1} are staged from register set u%2 into the buffers
+  //      that iteration u - 1 finished reading;
+  //   B: P V of tile u (V^T in buffer u%2) while tile u + 1 is masked (DIAG)
+  //      and max-reduced; then K_{u+4} / V_{u+3} are fetched into register
+  //      set u%2;
+  // rows whose max grew are rescaled after the block.  The mask is applied
+  // only by the DIAG form (tiles that reach the diagonal or the sequence end),
+  // and waves past their last tile only stage (stage_only), so the three
+  // loops below keep every step free of branches.  Barriers match by count:
   // every wave runs the same (even) number of iterations.  Staging is
   // unconditional, so the loop carries the register sets without copies (a
   // copy of a pending load would wait for every load in flight); tiles past
   // the end are zero-filled and written to buffers nobody reads again.
-  auto step = [&](const int u, const int set, floatx16 &s_cur, floatx16 &s_nxt) {
+  auto step = [&](const int u, const int set, floatx16 &s_cur, floatx16 &s_nxt, auto diag) {
+    constexpr bool DIAG = decltype(diag)::value;
     lds_barrier();
     const int kt = KSPLIT * u + kh;  // key tile
-    if (kt < n_wtiles) {
-      if constexpr (!PRESCALED) {  // raw scores -> log2 units, relative to m
+    const uint16_t *kp = &ks_h[((u + 1) & 1) * KS_SIZE + r32 * KS_PITCH + 8 * hf];
+    // V^T fragment (dt, kk): lane l = 16 q + s of group q takes dims 32 dt +
+    // 16 (q & 1) + 0..15 and keys 16 kk + 4 (q >> 1) + 0..3 (first read) and
+    // + 8 (second); it points at key ... + s / 4, dims ... + 4 (s % 4).
+    const int q4 = lane >> 4, s16 = lane & 15;
+    const uint16_t *vp = &vs_h[(u & 1) * VS_SIZE + (4 * (q4 >> 1) + (s16 >> 2)) * VS_PITCH +
+                               16 * (q4 & 1) + 4 * (s16 & 3)];
+    u32x4 kf[8];
+    u32x4 vf[8];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s_cur[e] = __builtin_fmaf(s_cur[e], c, -m_run);
+    for (int i = 0; i < 8; ++i) kf[i] = *reinterpret_cast<const u32x4 *>(kp + 16 * i);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+      {
+        const u32x2 lo = ds_read_tr16(vp + 16 * kk * VS_PITCH + 32 * dt);
+        const u32x2 hi = ds_read_tr16(vp + (16 * kk + 8) * VS_PITCH + 32 * dt);
+        vf[dt * 2 + kk] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
-      if (kt >= n_full) {  // diagonal / end-of-sequence tile
-        const int l2 = lim - kt * PF_BN;
+    // ---- A
+    s_nxt = mfma32<T>(kf[0], qreg[0], acc0);
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if (8 * (e >> 2) + (e & 3) > l2) s_cur[e] = -INFINITY;
-      }
-      float mx = -INFINITY;
+    for (int i = 1; i < 8; ++i) s_nxt = mfma32<T>(kf[i], qreg[i], s_nxt);
+    u32x4 pk[2];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s_cur[e]);
-      mx = fmaxf(mx, xor32_max(mx));
-      // set the running max at the row's first unmasked key, raise it when p
-      // would exceed 2^TAU
-      const bool grow = m_set ? mx > RESCALE_TAU : mx > -INFINITY;
-      if (__builtin_expect(__ballot(grow) != 0, 0)) {
-        const float d = grow ? mx : 0.f;
-        const float alpha = m_set ? fast_exp2(-d) : 0.f;
-        l_i *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s_cur[e] -= d;
-        m_run += d;
-        m_set = m_set || grow;
-      }
-
-      // ---- one straight-line block: scores of tile u+1 || exp + P V of tile u.
-      // All LDS operands of the block are fetched first (K fragments of tile
-      // u+1, V^T fragments of tile u), so their latency overlaps the first
-      // MFMAs and the exp work instead of stalling each MFMA in turn.
-      const uint16_t *kp = &ks_h[((u + 1) & 1) * KS_SIZE + r32 * KS_PITCH + 8 * hf];
-      const uint16_t *vp = &vt_h[(u & 1) * VT_SIZE + r32 * VT_PITCH + 8 * hf];
-      u32x4 kf[8];
-      u32x4 vf[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        kf[i] = *reinterpret_cast<const u32x4 *>(kp + 16 * i);
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-          vf[dt * 2 + kk] =
-              *reinterpret_cast<const u32x4 *>(vp + dt * 32 * VT_PITCH + 16 * kk);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int e = 0; e < 16; ++e) s_nxt[e] = PRESCALED ? -m_run : 0.f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s_nxt = mfma32<T>(kf[i], qreg[i], s_nxt);
-      u32x4 pk[2];
-#pragma unroll
-      for (int e2 = 0; e2 < 8; ++e2) {
-        const float p0 = fast_exp2(s_cur[2 * e2]);
-        const float p1 = fast_exp2(s_cur[2 * e2 + 1]);
-        const uint32_t pp = T::pack_p(p0, p1);
-        l_i = T::dot2(pp, ones, l_i);
-        pk[e2 >> 2][e2 & 3] = pp;
-      }
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-          o[dt] = mfma32<T>(vf[dt * 2 + kk], pk[kk], o[dt]);
-      PF_SCHEDULE();
+    for (int e2 = 0; e2 < 8; ++e2) {
+      const float p0 = fast_exp2(s_cur[2 * e2]);
+      const float p1 = fast_exp2(s_cur[2 * e2 + 1]);
+      const uint32_t pp = T::pack_p(p0, p1);
+      l_i = T::dot2(pp, ones, l_i);
+      pk[e2 >> 2][e2 & 3] = pp;
     }
-    // stage K_{u+2} into buffer u%2 (read as K_u in iteration u-1) and
-    // V_{u+1} into buffer (u+1)%2 (read as V_{u-1} in iteration u-1)
-    store_k(set, ks_h + (u & 1) * KS_SIZE);
-    store_v(set, vt_h + ((u + 1) & 1) * VT_SIZE);
-    load_k(set, u + 4);
-    load_v(set, u + 3);
+    store_k(kreg[set], ks_h + (u & 1) * KS_SIZE);
+    store_v(vreg[set], vs_h + ((u + 1) & 1) * VS_SIZE);
+    // ---- B
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) o[dt] = mfma32<T>(vf[dt * 2 + kk], pk[kk], o[dt]);
+    if constexpr (!PRESCALED) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s_nxt[e] = __builtin_fmaf(s_nxt[e], c, -m_run);
+    }
+    if constexpr (DIAG) {
+      const int l2 = lim - (kt + KSPLIT) * PF_BN;
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        if (8 * (e >> 2) + (e & 3) > l2) s_nxt[e] = -INFINITY;
+    }
+    const float mx = rowmax(s_nxt);
+    load_k(kreg[set], u + 4);
+    load_v(vreg[set], u + 3);
+    PF_SCHEDULE();
+    if (__builtin_expect(__ballot(mx > thr) != 0, 0)) rescale(mx, s_nxt);
   };
-  for (int u = 0; u < n_iter; u += 2) {
-    step(u, 0, s_a, s_b);
-    step(u + 1, 1, s_b, s_a);
+  auto stage_only = [&](const int u, const int set) {
+    lds_barrier();
+    store_k(kreg[set], ks_h + (u & 1) * KS_SIZE);
+    store_v(vreg[set], vs_h + ((u + 1) & 1) * VS_SIZE);
+    load_k(kreg[set], u + 4);
+    load_v(vreg[set], u + 3);
+  };
+  // step u needs the mask from u_first on (its next tile KSPLIT (u+1) + kh
+  // reaches n_full); tile KSPLIT u + kh is past this wave's rows from u_end on
+  const int nf_rel = n_full - kh, nw_rel = n_wtiles - kh;
+  const int u_first = nf_rel <= KSPLIT ? 0 : (nf_rel + KSPLIT - 1) / KSPLIT - 1;
+  const int u_end = nw_rel <= 0 ? 0 : (nw_rel + KSPLIT - 1) / KSPLIT;
+  const int u1 = u_first & ~1;                      // <= u_end <= n_iter
+  const int u2 = max(u1, min((u_end + 1) & ~1, n_iter));
+  const std::integral_constant<bool, false> plain;
+  const std::integral_constant<bool, true> diag;
+  int u = 0;
+  for (; u < u1; u += 2) {
+    step(u, 0, s_a, s_b, plain);
+    step(u + 1, 1, s_b, s_a, plain);
+  }
+  for (; u < u2; u += 2) {
+    step(u, 0, s_a, s_b, diag);
+    step(u + 1, 1, s_b, s_a, diag);
+  }
+  for (; u < n_iter; u += 2) {
+    stage_only(u, 0);
+    stage_only(u + 1, 1);
   }
 
   // ---- merge the key streams through LDS (KSPLIT = 2), normalise, store.
   // Stream 1 publishes (m, l, O) per lane; stream 0 rescales both states to
   // the larger max, adds them and writes the rows.  O^T is exchanged
   // register-major (64 lanes x 4 bytes contiguous per register).
-  float m0 = m_set ? m_run : -INFINITY, a0 = 1.f, l_own = l_i;
+  float m0 = thr > -INFINITY ? m_run : -INFINITY, a0 = 1.f, l_own = l_i;
   const float *xo = nullptr;
   float a1 = 0.f;
   if constexpr (KSPLIT == 2) {
