@@ -166,6 +166,33 @@ def test_workspace_reuse_across_shapes(dev):
             check(case, dev)
 
 
+def test_split_decode_graph_replays(dev):
+    """Split-K decode (decode + merge launches, torch-allocated workspace)
+    captured in a HIP graph and replayed several times, with eager calls of
+    another shape in between: every replay equals the eager result bit for
+    bit."""
+    case = make_decode_case(44, 6, [3000, 129, 4096, 0, 2048, 1500])
+    other = make_decode_case(45, 3, [5000, 64, 2200])
+    q, kc, vc, bt, cl = (t.to(dev) for t in (case.query, case.key_cache, case.value_cache,
+                                             case.block_tables, case.context_lens))
+    mb, bs = bt.shape[1], kc.shape[1]
+    eager = ops.paged_attention_decode(q, kc, vc, bt, cl, mb, bs, case.scale)
+    s = torch.cuda.Stream(device=dev)
+    s.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s):
+        ops.paged_attention_decode(q, kc, vc, bt, cl, mb, bs, case.scale)
+    torch.cuda.current_stream(dev).wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = ops.paged_attention_decode(q, kc, vc, bt, cl, mb, bs, case.scale)
+    other_ref = run_gpu(other, dev)
+    for _ in range(4):
+        g.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(out, eager)
+        assert torch.equal(run_gpu(other, dev), other_ref)
+
+
 def test_cfg2_repeat_calls_identical(dev):
     """Back-to-back calls on the same inputs give bit-identical outputs."""
     case = make_decode_case(43, 16, [4096, 1000, 300, 2500] * 4)
