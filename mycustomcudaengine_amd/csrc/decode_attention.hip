@@ -142,7 +142,10 @@ __device__ inline u32x4 ld_nt(const uint16_t *p) {
 template <class T, int G>
 __global__ __launch_bounds__(NT_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
 void paged_decode_kernel(DecodeArgs a) {
-  const int hgrp = blockIdx.x, j = blockIdx.y;
+  // per-sequence mode: blockIdx.x = slice * Hkv + kv head (the gsplit
+  // workgroups of one kv head share an XCD when Hkv is a multiple of 8)
+  const int gsub = a.per_seq ? (int)blockIdx.x / a.Hkv : 0;  // query-head slice
+  const int hgrp = a.per_seq ? (int)blockIdx.x % a.Hkv : (int)blockIdx.x, j = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15, lg = lane >> 4;
@@ -152,11 +155,13 @@ void paged_decode_kernel(DecodeArgs a) {
   const int hl = w % hpg, rlane = w / hpg;       // head in group, tile lane
   const int g = hgrp * hpg + hl;                 // this wave's kv head
   const bool active = rlane < wph && g < a.Hkv;  // uniform per wave
-  const int head0 = g * G;
+  const int gq = a.Hq / a.Hkv;                   // query heads per kv head
+  const int head0 = g * gq + gsub * G;           // this wave's G query heads
 
   __shared__ int pre[MAX_BATCH + 1];
   __shared__ int wave_tot[DEC_NW];
   __shared__ int blk_lds[MAX_IDS];
+  const int nb_hi = (int)(a.num_blocks - 1 < 0x7fffffff ? a.num_blocks - 1 : 0x7fffffff);
   __shared__ float red_acc[DEC_NW][G][HD];
   __shared__ float red_m[DEC_NW][G], red_l[DEC_NW][G];
 
@@ -165,7 +170,14 @@ void paged_decode_kernel(DecodeArgs a) {
     seg0 = 0;
     // one workgroup per (head group, sequence j): a one-sequence tile space
     // [0, tiles of j), so the segment loop below runs once with nparts == 1
-    // and the rows are written directly (no merge pass)
+    // and the rows are written directly (no merge pass).  The sequence's
+    // block ids (at most PER_SEQ_MAX_TOKENS / MIN_BS of them) are fetched
+    // together with its context length.
+    const int32_t *btj = a.btab + (int64_t)j * a.maxb;
+    for (int i = tid; i < a.maxb; i += NT_THREADS) {
+      const int v = btj[i];
+      blk_lds[i] = v < 0 ? 0 : (v > nb_hi ? nb_hi : v);
+    }
     if (tid == 0) {
       pre[j] = 0;
       pre[j + 1] = (clamp_ctx(a.ctx_lens[j], cap) + TILE - 1) / TILE;
@@ -174,9 +186,8 @@ void paged_decode_kernel(DecodeArgs a) {
     NT = pre[j + 1];
     je = 1;
     if (NT == 0) {
-      const int h_lo = hgrp * hpg * G, h_hi = min(a.Hkv, (hgrp + 1) * hpg) * G;
-      for (int i = tid; i < (h_hi - h_lo) * HD; i += NT_THREADS)
-        a.out[((int64_t)j * a.Hq + h_lo) * HD + i] = 0;
+      for (int i = tid; i < G * HD; i += NT_THREADS)
+        a.out[((int64_t)j * a.Hq + head0) * HD + i] = 0;
       return;
     }
   } else {
@@ -218,7 +229,6 @@ void paged_decode_kernel(DecodeArgs a) {
   const int64_t slot_stride = (int64_t)a.Hkv * HD;  // elements between slots
   const uint16_t *kbase = a.kcache + (int64_t)g * HD;
   const uint16_t *vbase = a.vcache + (int64_t)g * HD;
-  const int nb_hi = (int)(a.num_blocks - 1 < 0x7fffffff ? a.num_blocks - 1 : 0x7fffffff);
 
   for (; b < a.B && pre[b] < t_hi; ++b) {
     const int r0 = pre[b] + seg0;  // first real tile of b in the split space
@@ -259,14 +269,18 @@ void paged_decode_kernel(DecodeArgs a) {
     const int sub_tokens = max(TILE, ((MAX_IDS - 1) << bs_log2) / TILE * TILE);
     for (int s_lo = tok_lo; s_lo < tok_end; s_lo += sub_tokens) {
       const int t_end = min(s_lo + sub_tokens, tok_end);
-      const int first_blk = s_lo >> bs_log2;
-      const int nblk = ((t_end - 1) >> bs_log2) - first_blk + 1;
-      lds_barrier();  // previous users of blk_lds are done
-      for (int i = tid; i < nblk; i += NT_THREADS) {
-        const int v = bt[first_blk + i];
-        blk_lds[i] = v < 0 ? 0 : (v > nb_hi ? nb_hi : v);
+      // ids[blk - first_blk]: physical block of logical block blk of b (the
+      // per-sequence mode staged the whole row at the start)
+      const int first_blk = a.per_seq ? 0 : s_lo >> bs_log2;
+      if (!a.per_seq) {
+        const int nblk = ((t_end - 1) >> bs_log2) - first_blk + 1;
+        lds_barrier();  // previous users of blk_lds are done
+        for (int i = tid; i < nblk; i += NT_THREADS) {
+          const int v = bt[first_blk + i];
+          blk_lds[i] = v < 0 ? 0 : (v > nb_hi ? nb_hi : v);
+        }
+        lds_barrier();
       }
-      lds_barrier();
       if (!active) continue;
 
       // ---- loads of one tile: lane group lg owns tokens t0 + 8 lg .. +7 (one
@@ -454,7 +468,7 @@ void paged_decode_kernel(DecodeArgs a) {
         L += red_l[hh + r * hpg][h] * sc;
         A += red_acc[hh + r * hpg][h][d] * sc;
       }
-      const int64_t row = (int64_t)b * a.Hq + (hgrp * hpg + hh) * G + h;
+      const int64_t row = (int64_t)b * a.Hq + (hgrp * hpg + hh) * gq + gsub * G + h;
       if (nparts == 1) {
         a.out[row * HD + d] = T::from_float(A / L);
       } else {
@@ -640,20 +654,32 @@ extern "C" int mce_paged_attention_decode(
   // contexts use the balanced split over the concatenated tile space.
   const bool per_seq = (int64_t)max_blocks_per_seq * block_size <= PER_SEQ_MAX_TOKENS;
   a.per_seq = per_seq ? 1 : 0;
+  // Per-sequence mode on a grid that leaves CUs idle (few sequences x kv
+  // heads): the query heads of a kv head are split over gsplit workgroups
+  // (the largest divisor of G that still fits the CUs).  Each reads the same
+  // K/V pages (the repeats come from L2 / the infinity cache) and does 1/gsplit
+  // of the score and P V work, which is what bounds this mode.
+  int gsplit = 1;
   if (per_seq) {
     a.hpg = 1;
     a.wph = DEC_NW;
+    for (int d = G; d > 1; --d)
+      if (G % d == 0 && (int64_t)batch * num_kv_heads * d <= cu_count()) {
+        gsplit = d;
+        break;
+      }
   }
+  const int Gw = G / gsplit;  // query heads per wave
   a.num_blocks = num_blocks;
   a.scale_log2 = scale * 1.4426950408889634f;
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid = per_seq ? dim3(num_kv_heads, batch) : dim3(Lay.groups, Lay.J);
+  const dim3 grid = per_seq ? dim3(num_kv_heads * gsplit, batch) : dim3(Lay.groups, Lay.J);
 #define MCE_DEC_CASE(TT, GG)                                                   \
   case GG:                                                                     \
     paged_decode_kernel<TT, GG><<<grid, NT_THREADS, 0, st>>>(a);               \
     break;
 #define MCE_DEC_LAUNCH(TT)                                                     \
-  switch (G) {                                                                 \
+  switch (Gw) {                                                                \
     MCE_DEC_CASE(TT, 1)                                                        \
     MCE_DEC_CASE(TT, 2)                                                        \
     MCE_DEC_CASE(TT, 3)                                                        \

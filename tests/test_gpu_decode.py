@@ -61,6 +61,17 @@ def test_gqa_groups(dev, hq, hkv):
     check(make_decode_case(7 + hq, 3, [300, 17, 1100], num_heads=hq, num_kv_heads=hkv), dev)
 
 
+@pytest.mark.parametrize("hq,hkv,b", [(8, 8, 3), (24, 8, 3), (24, 8, 8), (32, 8, 16), (48, 8, 8),
+                                      (64, 8, 8), (64, 8, 4), (6, 2, 5), (3, 1, 7), (24, 8, 40)])
+def test_gqa_groups_per_sequence_mode(dev, hq, hkv, b):
+    """Contexts within 1024 tokens of table capacity (one workgroup per
+    sequence and kv head, or per query-head slice of a kv head when the grid
+    would leave CUs idle): every split of the G query heads, including none."""
+    ctxs = torch.randint(1, 641, (b,), generator=torch.Generator().manual_seed(hq * 100 + b))
+    check(make_decode_case(60 + hq + b, b, ctxs.tolist(), num_heads=hq, num_kv_heads=hkv,
+                           max_blocks=40), dev)
+
+
 @pytest.mark.parametrize("bs", [8, 16, 32, 64, 256])
 def test_block_sizes(dev, bs):
     check(make_decode_case(11 + bs, 3, [700, 5, 1500], block_size=bs), dev)
