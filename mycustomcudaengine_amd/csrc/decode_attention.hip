@@ -494,11 +494,16 @@ __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
   const int64_t row = (int64_t)b * a.Hq + h;
   const float *ml = a.ws_ml + row * a.J * 2;
   const float *ac = a.ws_acc + row * a.J * HD + d;
-  // The part count and the first HD parts' (m, l) are loaded together (one
-  // memory round trip); slots at or past the count are ignored (the
-  // workspace holds J >= parts slots per row, so these reads stay inside it).
+  // The part count, the first HD parts' (m, l) and this lane's dim of the
+  // first SPEC parts' partial outputs are loaded together (one memory round
+  // trip); slots at or past the count are never used (the workspace holds
+  // J >= parts slots per row, so these reads stay inside it).
+  constexpr int SPEC = 16;
   const int n_raw = a.ws_nparts[b];
   const float2 ml0 = d < a.J ? *reinterpret_cast<const float2 *>(ml + 2 * d) : float2{0.f, 0.f};
+  float v0[SPEC];
+#pragma unroll
+  for (int k = 0; k < SPEC; ++k) v0[k] = k < a.J ? ac[(int64_t)k * HD] : 0.f;
   const int n = __builtin_amdgcn_readfirstlane(n_raw);
   if (n <= 1) return;
   __shared__ float w_lds[HD], wl_lds[HD], mx_lds[2];
@@ -527,6 +532,15 @@ __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
     A *= sc;
     L *= sc;
     int i = 0;
+    if (c0 == 0) {  // the prefetched parts (selects, not products: unused slots may hold NaN)
+#pragma unroll
+      for (int k = 0; k < SPEC; ++k)
+        if (k < cn) {
+          A += w_lds[k] * v0[k];
+          L += wl_lds[k];
+        }
+      i = min(SPEC, cn);
+    }
     for (; i + 8 <= cn; i += 8) {
       float v[8];
 #pragma unroll
