@@ -96,7 +96,7 @@ MCE_API int mce_paged_kv_store(int dtype, const void *key, const void *value,
 /*
  * Workspace bytes mce_paged_attention_decode needs for these dimensions
  * (split-K partial softmax state).  Depends only on host-known sizes;
- * 0 means no workspace is needed.
+ * 0 means no workspace is needed (table capacities of at most 1024 tokens).
  */
 MCE_API size_t mce_paged_attention_decode_workspace_size(int batch, int num_heads,
                                                  int num_kv_heads,
@@ -132,6 +132,33 @@ MCE_API int mce_paged_attention_decode(int dtype, const void *query,
                                int block_size, int64_t num_blocks, float scale,
                                void *workspace, size_t workspace_bytes,
                                void *stream);
+
+/*
+ * One decode token per sequence with the rotary embedding and the paged
+ * store of the new token fused in: rotates query[b] and key[b] at
+ * positions[b] (rows of cos/sin_table as in mce_rope_inplace; positions
+ * outside [0, table_rows) are not rotated), writes the rotated key and value
+ * to the page slot slot_mapping[b] (skipped when outside the pool), then
+ * computes mce_paged_attention_decode with the rotated query.  Outputs and
+ * caches are bit-identical to mce_rope_kv_store (query_out given) followed by
+ * mce_paged_attention_decode.  query/key/value are [batch, heads, head_dim]
+ * rows q_stride / kv_stride elements apart (views into one fused projection
+ * output).  Only for table capacities (max_blocks_per_seq * block_size) of
+ * at most 1024 tokens, the per-sequence mode; larger ones return
+ * MCE_ERR_UNSUPPORTED.  No workspace.  No single counterpart in the
+ * reference: it fuses the three calls of its decode step
+ * (engine/models/llama.py:117-134: rope_inplace, paged_kv_store,
+ * paged_attention_decode).
+ */
+MCE_API int mce_paged_attention_decode_rope(int dtype, const void *query, const void *key,
+                                    const void *value, void *key_cache, void *value_cache,
+                                    const float *cos_table, const float *sin_table,
+                                    const int32_t *positions, const int32_t *slot_mapping,
+                                    const int32_t *block_tables, const int32_t *context_lens,
+                                    void *output, int batch, int num_heads, int num_kv_heads,
+                                    int head_dim, int max_blocks_per_seq, int block_size,
+                                    int64_t num_blocks, int64_t table_rows, int64_t q_stride,
+                                    int64_t kv_stride, float scale, void *stream);
 
 /*
  * In-place rotary embedding (half-split / rotate_half form), i < head_dim/2:

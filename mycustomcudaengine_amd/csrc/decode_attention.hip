@@ -71,7 +71,7 @@ constexpr int PER_SEQ_MAX_TOKENS = 1024;
 
 
 struct DecodeArgs {
-  const uint16_t *query;    // [B, Hq, HD]
+  const uint16_t *query;    // [B, Hq, HD] rows q_stride_b elements apart
   const uint16_t *kcache;   // [NB, BS, Hkv, HD]
   const uint16_t *vcache;
   const int32_t *btab;      // [B, maxb]
@@ -83,6 +83,15 @@ struct DecodeArgs {
   int B, Hq, Hkv, maxb, bs_log2, J;
   int hpg, wph;             // kv heads per workgroup, waves per kv head
   int per_seq;              // 1: workgroup (group, b) covers all of sequence b
+  int64_t q_stride_b;       // elements between the query rows of two sequences
+  // Fused RoPE + KV append (per-sequence mode; knew == nullptr: off): the
+  // query is rotated in registers, and k (rotated) and v of the new token are
+  // written to the page slot before the attention reads the sequence.
+  const uint16_t *knew, *vnew;  // [B, Hkv, HD] rows new_stride_b elements apart
+  int64_t new_stride_b;
+  const float *rope_cos, *rope_sin;  // [table_rows, HD / 2]
+  const int32_t *positions, *slots;  // [B]
+  int64_t table_rows, num_slots;
   int64_t num_blocks;
   float scale_log2;
 };
@@ -137,6 +146,39 @@ __device__ inline u32x4 ld_nt(const uint16_t *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 }
 
+// RoPE of one 128-dim head row spread over a 16-lane group: lane lr holds
+// dims 8 lr .. 8 lr + 7; the rotation pairs dim i < 64 with i + 64, i.e. lane
+// lr with lane lr ^ 8 (all 64 lanes take part in the exchange).  Returns the
+// lane's rotated 8 values, rounded as rope_inplace rounds them.
+template <class T>
+__device__ inline u32x4 rope_rows(const u32x4 x, const DecodeArgs &a, int pos, int lr) {
+  u32x4 pt;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) pt[k] = (uint32_t)__shfl_xor((int)x[k], 8, 64);
+  const bool lo_half = lr < 8;
+  const int i0 = 8 * (lr & 7);  // rotation index of the lane's first dim
+  const float *cp = a.rope_cos + (int64_t)pos * (HD / 2) + i0;
+  const float *sp = a.rope_sin + (int64_t)pos * (HD / 2) + i0;
+  const floatx4 c0 = *reinterpret_cast<const floatx4 *>(cp);
+  const floatx4 c1 = *reinterpret_cast<const floatx4 *>(cp + 4);
+  const floatx4 s0 = *reinterpret_cast<const floatx4 *>(sp);
+  const floatx4 s1 = *reinterpret_cast<const floatx4 *>(sp + 4);
+  u32x4 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float cl = k < 2 ? c0[2 * k] : c1[2 * k - 4], ch = k < 2 ? c0[2 * k + 1] : c1[2 * k - 3];
+    const float sl = k < 2 ? s0[2 * k] : s1[2 * k - 4], sh = k < 2 ? s0[2 * k + 1] : s1[2 * k - 3];
+    // (x0, x1) = (dim i, dim i + 64) of this element pair
+    const float a0 = T::lo(lo_half ? x[k] : pt[k]), a1 = T::lo(lo_half ? pt[k] : x[k]);
+    const float b0 = T::hi(lo_half ? x[k] : pt[k]), b1 = T::hi(lo_half ? pt[k] : x[k]);
+    float ra0, ra1, rb0, rb1;
+    rope_pair(a0, a1, cl, sl, ra0, ra1);
+    rope_pair(b0, b1, ch, sh, rb0, rb1);
+    o[k] = lo_half ? pack2<T>(ra0, rb0) : pack2<T>(ra1, rb1);
+  }
+  return o;
+}
+
 // Two waves per SIMD: one 8-wave workgroup per CU.  (GQA groups of 7 or 8
 // query heads per kv head spill a few registers at this occupancy.)
 template <class T, int G>
@@ -182,7 +224,28 @@ void paged_decode_kernel(DecodeArgs a) {
       pre[j] = 0;
       pre[j + 1] = (clamp_ctx(a.ctx_lens[j], cap) + TILE - 1) / TILE;
     }
-    lds_barrier();
+    if (a.knew) {
+      // The new token's k (rotated) and v into its page slot, by wave 0
+      // (lane lr: dims 8 lr .. 8 lr + 7, pair partner in lane lr ^ 8).  Every
+      // workgroup of this kv head writes the same bytes and only then reads
+      // the sequence, so each sees its own write.
+      if (w == 0) {
+        const int64_t slot = a.slots[j];
+        const int pos = a.positions[j];
+        const int64_t row = (int64_t)j * a.new_stride_b + (int64_t)g * HD + lr * 8;
+        u32x4 kx = *reinterpret_cast<const u32x4 *>(a.knew + row);
+        const u32x4 vx = *reinterpret_cast<const u32x4 *>(a.vnew + row);
+        if (pos >= 0 && pos < a.table_rows) kx = rope_rows<T>(kx, a, pos, lr);
+        if (lg == 0 && slot >= 0 && slot < a.num_slots) {
+          const int64_t dst = (slot * a.Hkv + g) * HD + lr * 8;
+          *reinterpret_cast<u32x4 *>(const_cast<uint16_t *>(a.kcache) + dst) = kx;
+          *reinterpret_cast<u32x4 *>(const_cast<uint16_t *>(a.vcache) + dst) = vx;
+        }
+      }
+      __syncthreads();  // the slot's stores are complete before any K/V load
+    } else {
+      lds_barrier();
+    }
     NT = pre[j + 1];
     je = 1;
     if (NT == 0) {
@@ -247,8 +310,15 @@ void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int h = 0; h < G; ++h)
       qv[h] = active ? *reinterpret_cast<const u32x4 *>(
-                           a.query + ((int64_t)b * a.Hq + head0 + h) * HD + lr * 8)
+                           a.query + (int64_t)b * a.q_stride_b + (int64_t)(head0 + h) * HD + lr * 8)
                      : u32x4{0, 0, 0, 0};
+    if (a.knew) {  // fused RoPE of the query (same rounding as rope_inplace)
+      const int pos = a.positions[b];
+      if (pos >= 0 && pos < a.table_rows) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) qv[h] = rope_rows<T>(qv[h], a, pos, lr);
+      }
+    }
 
     // m_run: running max of the raw scores (uniform over the wave);
     // l_grp: softmax denominator of this lane group's tokens;
@@ -592,16 +662,25 @@ extern "C" size_t mce_paged_attention_decode_workspace_size(
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 ||
       max_blocks_per_seq <= 0 || block_size <= 0)
     return 0;
+  // short contexts run the per-sequence mode, which needs no workspace
+  if ((int64_t)max_blocks_per_seq * block_size <= PER_SEQ_MAX_TOKENS) return 0;
   return decode_layout(batch, num_heads, num_kv_heads).total;
 }
 
-extern "C" int mce_paged_attention_decode(
-    int dtype, const void *query, const void *key_cache,
-    const void *value_cache, const int32_t *block_tables,
-    const int32_t *context_lens, void *output, int batch, int num_heads,
-    int num_kv_heads, int head_dim, int max_blocks_per_seq, int block_size,
-    int64_t num_blocks, float scale, void *workspace, size_t workspace_bytes,
-    void *stream) {
+namespace {
+struct FusedRope {  // fused RoPE + KV append operands (null knew: off)
+  const void *knew = nullptr, *vnew = nullptr;
+  int64_t q_stride_b = 0, new_stride_b = 0;
+  const float *cos = nullptr, *sin = nullptr;
+  const int32_t *positions = nullptr, *slots = nullptr;
+  int64_t table_rows = 0;
+};
+
+int decode_impl(int dtype, const void *query, const void *key_cache, const void *value_cache,
+                const int32_t *block_tables, const int32_t *context_lens, void *output, int batch,
+                int num_heads, int num_kv_heads, int head_dim, int max_blocks_per_seq,
+                int block_size, int64_t num_blocks, float scale, void *workspace,
+                size_t workspace_bytes, void *stream, const FusedRope &fr) {
   clear_error();
   MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16,
               "mce_paged_attention_decode: unknown dtype %d", dtype);
@@ -637,23 +716,34 @@ extern "C" int mce_paged_attention_decode(
                   ((int64_t)1 << 30),
               "mce_paged_attention_decode: batch x context too large");
   const DecodeLayout Lay = decode_layout(batch, num_heads, num_kv_heads);
-  if (workspace == nullptr || workspace_bytes < Lay.total ||
-      (reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+  const bool per_seq = (int64_t)max_blocks_per_seq * block_size <= PER_SEQ_MAX_TOKENS;
+  if (!per_seq && (workspace == nullptr || workspace_bytes < Lay.total ||
+                   (reinterpret_cast<uintptr_t>(workspace) & 255) != 0))
     return set_error(MCE_ERR_WORKSPACE,
                      "mce_paged_attention_decode: a 256-byte aligned workspace of %zu bytes "
                      "is required (%zu given)",
                      Lay.total, workspace_bytes);
   DecodeArgs a{};
   a.query = (const uint16_t *)query;
+  a.q_stride_b = fr.knew ? fr.q_stride_b : (int64_t)num_heads * head_dim;
+  a.knew = (const uint16_t *)fr.knew;
+  a.vnew = (const uint16_t *)fr.vnew;
+  a.new_stride_b = fr.new_stride_b;
+  a.rope_cos = fr.cos;
+  a.rope_sin = fr.sin;
+  a.positions = fr.positions;
+  a.slots = fr.slots;
+  a.table_rows = fr.table_rows;
+  a.num_slots = num_blocks * block_size;
   a.kcache = (const uint16_t *)key_cache;
   a.vcache = (const uint16_t *)value_cache;
   a.btab = block_tables;
   a.ctx_lens = context_lens;
   a.out = (uint16_t *)output;
-  char *base = (char *)workspace;
-  a.ws_ml = (float *)(base + Lay.ml_off);
-  a.ws_acc = (float *)(base + Lay.acc_off);
-  a.ws_nparts = (int *)(base + Lay.nparts_off);
+  char *base = (char *)workspace;  // unused (may be null) in per-sequence mode
+  a.ws_ml = per_seq ? nullptr : (float *)(base + Lay.ml_off);
+  a.ws_acc = per_seq ? nullptr : (float *)(base + Lay.acc_off);
+  a.ws_nparts = per_seq ? nullptr : (int *)(base + Lay.nparts_off);
   a.B = batch;
   a.Hq = num_heads;
   a.Hkv = num_kv_heads;
@@ -666,7 +756,6 @@ extern "C" int mce_paged_attention_decode(
   // sequence (at most PER_SEQ_MAX_TOKENS x 512 bytes of K/V) and writes the
   // final rows, so the launch is one kernel with no partials.  Longer
   // contexts use the balanced split over the concatenated tile space.
-  const bool per_seq = (int64_t)max_blocks_per_seq * block_size <= PER_SEQ_MAX_TOKENS;
   a.per_seq = per_seq ? 1 : 0;
   // Per-sequence mode on a grid that leaves CUs idle (few sequences x kv
   // heads): the query heads of a kv head are split over gsplit workgroups
@@ -712,4 +801,54 @@ extern "C" int mce_paged_attention_decode(
 #undef MCE_DEC_LAUNCH
 #undef MCE_DEC_CASE
   return check_launch("mce_paged_attention_decode");
+}
+}  // namespace
+
+extern "C" int mce_paged_attention_decode(
+    int dtype, const void *query, const void *key_cache,
+    const void *value_cache, const int32_t *block_tables,
+    const int32_t *context_lens, void *output, int batch, int num_heads,
+    int num_kv_heads, int head_dim, int max_blocks_per_seq, int block_size,
+    int64_t num_blocks, float scale, void *workspace, size_t workspace_bytes,
+    void *stream) {
+  return decode_impl(dtype, query, key_cache, value_cache, block_tables, context_lens, output,
+                     batch, num_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size,
+                     num_blocks, scale, workspace, workspace_bytes, stream, FusedRope{});
+}
+
+extern "C" int mce_paged_attention_decode_rope(
+    int dtype, const void *query, const void *key, const void *value, void *key_cache,
+    void *value_cache, const float *cos_table, const float *sin_table, const int32_t *positions,
+    const int32_t *slot_mapping, const int32_t *block_tables, const int32_t *context_lens,
+    void *output, int batch, int num_heads, int num_kv_heads, int head_dim,
+    int max_blocks_per_seq, int block_size, int64_t num_blocks, int64_t table_rows,
+    int64_t q_stride, int64_t kv_stride, float scale, void *stream) {
+  clear_error();
+  if ((int64_t)max_blocks_per_seq * block_size > PER_SEQ_MAX_TOKENS)
+    return set_error(MCE_ERR_UNSUPPORTED,
+                     "mce_paged_attention_decode_rope: table capacity %lld tokens > %d (use "
+                     "mce_rope_kv_store + mce_paged_attention_decode)",
+                     (long long)max_blocks_per_seq * block_size, PER_SEQ_MAX_TOKENS);
+  MCE_REQUIRE(batch == 0 || (key && value && cos_table && sin_table && positions && slot_mapping),
+              "mce_paged_attention_decode_rope: null pointer");
+  MCE_REQUIRE(table_rows >= 0, "mce_paged_attention_decode_rope: bad table_rows");
+  MCE_REQUIRE(q_stride >= (int64_t)num_heads * head_dim && q_stride % 8 == 0 &&
+                  kv_stride >= (int64_t)num_kv_heads * head_dim && kv_stride % 8 == 0,
+              "mce_paged_attention_decode_rope: bad row strides");
+  MCE_REQUIRE(batch == 0 || (aligned16(key) && aligned16(value) && aligned16(cos_table) &&
+                             aligned16(sin_table)),
+              "mce_paged_attention_decode_rope: k, v and the tables must be 16-byte aligned");
+  FusedRope fr;
+  fr.knew = key;
+  fr.vnew = value;
+  fr.q_stride_b = q_stride;
+  fr.new_stride_b = kv_stride;
+  fr.cos = cos_table;
+  fr.sin = sin_table;
+  fr.positions = positions;
+  fr.slots = slot_mapping;
+  fr.table_rows = table_rows;
+  return decode_impl(dtype, query, key_cache, value_cache, block_tables, context_lens, output,
+                     batch, num_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size,
+                     num_blocks, scale, nullptr, 0, stream, fr);
 }

@@ -249,10 +249,7 @@ __device__ inline void rope_rotate4(const uint16_t *p, int half, const float *c4
   float x1[4] = {T::lo(b[0]), T::hi(b[0]), T::lo(b[1]), T::hi(b[1])};
   float r0[4], r1[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    r0[k] = x0[k] * c4[k] - x1[k] * s4[k];
-    r1[k] = x0[k] * s4[k] + x1[k] * c4[k];
-  }
+  for (int k = 0; k < 4; ++k) rope_pair(x0[k], x1[k], c4[k], s4[k], r0[k], r1[k]);
   u32x2 oa, ob;
   oa[0] = pack2<T>(r0[0], r0[1]);
   oa[1] = pack2<T>(r0[2], r0[3]);

@@ -155,6 +155,16 @@ __device__ inline float wave_max(float v) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Rotary rotation of one (x_i, x_{i+D/2}) pair by (c, s), fp32: the single
+// definition every RoPE path uses.  Contraction into FMAs is off, so each
+// product and the sum round separately and every caller rounds identically
+// (the compiler would otherwise pick the fused operand per call site).
+__device__ inline void rope_pair(float x0, float x1, float c, float s, float &r0, float &r1) {
+#pragma clang fp contract(off)
+  r0 = x0 * c - x1 * s;
+  r1 = x0 * s + x1 * c;
+}
+
 // Workgroup barrier that orders LDS accesses only.  The fences are scoped to
 // the local (LDS) address space, so the wait before s_barrier covers this
 // wave's LDS operations (lgkmcnt) while global loads issued earlier stay in

@@ -17,11 +17,14 @@ matrix, so a layer runs 4 GEMMs instead of 7 and SwiGLU reads the gate/up
 GEMM output directly (the reference concatenates gate and up activations
 with torch.cat every step, llama.py:161).  The original weight names stay
 in `weights` as views into the fused matrices.  q/k/v are strided views of
-the fused projection output; one fused launch rotates q (into a contiguous
-buffer for the attention kernel) and k and writes k/v to their pages (the
-reference calls rope_inplace and paged_kv_store, llama.py:117-127), and the
-o_proj / down_proj GEMMs add into the residual stream in place (addmm_)
-instead of a separate add.
+the fused projection output.  When the block tables hold at most 1024 tokens
+(the decode attention's one-workgroup-per-sequence mode) one launch rotates
+q and k, writes k/v to their pages and runs the attention
+(decode_rope_attention); for longer tables one fused launch rotates q (into
+a contiguous buffer) and k and writes k/v to their pages, then the decode
+attention runs (the reference calls rope_inplace, paged_kv_store and
+paged_attention_decode, llama.py:117-134).  The o_proj / down_proj GEMMs add
+into the residual stream in place (addmm_) instead of a separate add.
 RoPE tables cover max_position_embeddings positions (capped at 131072)
 instead of the reference's fixed 4096 (llama.py:42).
 """
@@ -34,7 +37,7 @@ import torch
 
 import my_cuda_engine_cpp as ops
 
-from ...ops import rope_kv_store
+from ...ops import PER_SEQ_MAX_TOKENS, decode_rope_attention, rope_kv_store
 from ..cache import KVCacheManager
 
 ROPE_TABLE_CAP = 131072
@@ -129,18 +132,26 @@ class Llama3BEngineModel:
         hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
         x = self.weights["model.embed_tokens.weight"][input_ids.view(-1)]  # [B, hidden]
         kv = self.cache_manager.kv_cache
+        # tables of at most PER_SEQ_MAX_TOKENS: RoPE + KV append fused into attention
+        fused = max_blocks_per_seq * self.cache_manager.block_size <= PER_SEQ_MAX_TOKENS
         for l in range(c.num_hidden_layers):
             p = f"model.layers.{l}"
             xn = ops.rmsnorm(x, self.weights[f"{p}.input_layernorm.weight"], c.rms_norm_eps)
             q, k, v = self._attention_block_proj(l, xn)
-            q_rot = torch.empty(b, hq, d, dtype=q.dtype, device=q.device)
-            rope_kv_store(q.view(b, hq, d), k.view(b, hkv, d), v.view(b, hkv, d), kv[l, 0],
-                          kv[l, 1], self.cos_table, self.sin_table, positions.view(-1),
-                          slot_mapping, query_out=q_rot)
-            attn = ops.paged_attention_decode(q_rot, kv[l, 0], kv[l, 1],
-                                              block_tables_tensor, context_lens,
-                                              max_blocks_per_seq,
-                                              self.cache_manager.block_size, self.scale)
+            q3, k3, v3 = q.view(b, hq, d), k.view(b, hkv, d), v.view(b, hkv, d)
+            if fused:  # RoPE, KV append and attention in one launch
+                attn = decode_rope_attention(q3, k3, v3, kv[l, 0], kv[l, 1], self.cos_table,
+                                             self.sin_table, positions.view(-1), slot_mapping,
+                                             block_tables_tensor, context_lens,
+                                             max_blocks_per_seq, self.scale)
+            else:
+                q_rot = torch.empty(b, hq, d, dtype=q.dtype, device=q.device)
+                rope_kv_store(q3, k3, v3, kv[l, 0], kv[l, 1], self.cos_table, self.sin_table,
+                              positions.view(-1), slot_mapping, query_out=q_rot)
+                attn = ops.paged_attention_decode(q_rot, kv[l, 0], kv[l, 1],
+                                                  block_tables_tensor, context_lens,
+                                                  max_blocks_per_seq,
+                                                  self.cache_manager.block_size, self.scale)
             x.addmm_(attn.view(b, hq * d), self.weights[f"{p}.self_attn.o_proj.weight"].T)
             self._mlp(l, x)
         xf = ops.rmsnorm(x, self.weights["model.norm.weight"], c.rms_norm_eps)

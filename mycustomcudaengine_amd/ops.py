@@ -289,6 +289,72 @@ def rope_kv_store(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                   value.stride(0), value.stride(1), _stream(dev))
 
 
+PER_SEQ_MAX_TOKENS = 1024  # table capacity up to which decode runs one workgroup per sequence
+
+
+def decode_rope_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                          key_cache: torch.Tensor, value_cache: torch.Tensor,
+                          cos_table: torch.Tensor, sin_table: torch.Tensor,
+                          positions: torch.Tensor, slot_mapping: torch.Tensor,
+                          block_tables: torch.Tensor, context_lens: torch.Tensor,
+                          max_blocks_per_seq: int, scale: float) -> torch.Tensor:
+    """rope_inplace + paged_kv_store of the new token + paged_attention_decode
+    in one launch (engine/models/llama.py:117-134 makes the three calls);
+    outputs and caches bit-identical to rope_kv_store(query_out=...) followed
+    by paged_attention_decode.  query [B, Hq, D], key/value [B, Hkv, D] with
+    batch strides (views into a fused projection, head rows contiguous);
+    query and key are not modified.  Only for table capacities
+    (max_blocks_per_seq * block_size) up to PER_SEQ_MAX_TOKENS.
+    """
+    dev = _on_gpu("decode_rope_attention", query, key, value, key_cache, value_cache,
+                  cos_table, sin_table, positions, slot_mapping, block_tables, context_lens)
+    code = _dtype_code(query, "decode_rope_attention query")
+    for t, n in ((key, "key"), (value, "value"), (key_cache, "key_cache"),
+                 (value_cache, "value_cache")):
+        _check(t.dtype == query.dtype, f"decode_rope_attention: {n} dtype must match query")
+    _check(query.dim() == 3 and key.dim() == 3 and value.shape == key.shape and
+           key.size(0) == query.size(0) and key.size(2) == query.size(2),
+           "decode_rope_attention: query [B, Hq, D], key/value [B, Hkv, D] expected")
+    b, hq, d = query.shape
+    hkv = key.size(1)
+    for t, n in ((query, "query"), (key, "key"), (value, "value")):
+        _check(t.stride(2) == 1 and t.stride(1) == d,
+               f"decode_rope_attention: {n} heads must be contiguous rows of head_dim")
+    _check(key.stride(0) == value.stride(0),
+           "decode_rope_attention: key and value need the same batch stride")
+    _check(key_cache.dim() == 4 and key_cache.shape == value_cache.shape and
+           key_cache.size(2) == hkv and key_cache.size(3) == d and
+           key_cache.is_contiguous() and value_cache.is_contiguous(),
+           "decode_rope_attention: caches must be contiguous [num_blocks, block_size, Hkv, D]")
+    nb, bs = key_cache.shape[:2]
+    mb = int(max_blocks_per_seq)
+    _check(mb * bs <= PER_SEQ_MAX_TOKENS,
+           f"decode_rope_attention: table capacity {mb * bs} > {PER_SEQ_MAX_TOKENS}; use "
+           "rope_kv_store + paged_attention_decode")
+    for t, n in ((cos_table, "cos_table"), (sin_table, "sin_table")):
+        _check(t.dtype == torch.float32 and t.dim() == 2 and t.size(1) == d // 2 and
+               t.is_contiguous(), f"decode_rope_attention: {n} must be contiguous fp32 "
+               f"[P, {d // 2}]")
+    _check(cos_table.size(0) == sin_table.size(0), "decode_rope_attention: table lengths differ")
+    for t, n in ((positions, "positions"), (slot_mapping, "slot_mapping"),
+                 (context_lens, "context_lens")):
+        _check(t.dtype == torch.int32 and t.numel() == b and t.is_contiguous(),
+               f"decode_rope_attention: {n} must be contiguous int32 with {b} elements")
+    _check(block_tables.dtype == torch.int32 and block_tables.dim() == 2 and
+           block_tables.size(0) == b and block_tables.size(1) == mb and
+           block_tables.is_contiguous(),
+           f"decode_rope_attention: block_tables must be contiguous int32 [{b}, {mb}]")
+    out = torch.empty(b, hq, d, dtype=query.dtype, device=query.device)
+    with _on_device(dev):
+        _lib.call("mce_paged_attention_decode_rope", code, query.data_ptr(), key.data_ptr(),
+                  value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+                  cos_table.data_ptr(), sin_table.data_ptr(), positions.data_ptr(),
+                  slot_mapping.data_ptr(), block_tables.data_ptr(), context_lens.data_ptr(),
+                  out.data_ptr(), b, hq, hkv, d, mb, bs, nb, cos_table.size(0),
+                  query.stride(0), key.stride(0), float(scale), _stream(dev))
+    return out
+
+
 _EPILOGUES = {"store": 0, "add": 1, "swiglu": 2}
 
 

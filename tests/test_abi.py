@@ -15,7 +15,7 @@ HEADER_ENTRY_POINTS = {
     "mce_last_error", "mce_abi_version", "mce_rmsnorm", "mce_swiglu",
     "mce_paged_kv_store", "mce_paged_attention_decode_workspace_size",
     "mce_paged_attention_decode", "mce_rope_inplace", "mce_prefill_attention",
-    "mce_rope_kv_store", "mce_decode_gemm",
+    "mce_rope_kv_store", "mce_decode_gemm", "mce_paged_attention_decode_rope",
 }
 
 
@@ -70,7 +70,7 @@ def test_kv_store_validation(lib):
 
 def _decode(lib, **kw):
     args = dict(dtype=0, q=1 << 12, kc=1 << 12, vc=1 << 12, bt=1 << 12, cl=1 << 12,
-                out=1 << 12, B=2, Hq=24, Hkv=8, D=128, maxb=4, bs=16, nb=10, scale=0.088,
+                out=1 << 12, B=2, Hq=24, Hkv=8, D=128, maxb=128, bs=16, nb=10, scale=0.088,
                 ws=None, ws_bytes=0, stream=None)
     args.update(kw)
     a = args
@@ -95,8 +95,9 @@ def test_decode_validation(lib):
 
 def test_decode_workspace_size(lib):
     f = lib.mce_paged_attention_decode_workspace_size
-    assert f(0, 24, 8, 4, 16) == 0
-    small, big = f(1, 24, 8, 4, 16), f(32, 24, 8, 256, 16)
+    assert f(0, 24, 8, 128, 16) == 0
+    assert f(32, 24, 8, 64, 16) == 0  # <= 1024 tokens of capacity: per-sequence mode
+    small, big = f(1, 24, 8, 128, 16), f(32, 24, 8, 256, 16)
     assert 0 < small < big
     assert big % 256 == 0
 

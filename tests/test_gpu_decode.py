@@ -10,6 +10,7 @@ import pytest
 import torch
 
 import my_cuda_engine_cpp as ops
+from mycustomcudaengine_amd.ops import decode_rope_attention, rope_kv_store
 from oracle.inputs import cfg1_decode, cfg2_decode, cfg4_decode, make_decode_case
 from oracle.ops_ref import decode_attention_ref
 
@@ -202,6 +203,62 @@ def test_split_decode_graph_replays(dev):
         torch.cuda.synchronize(dev)
         assert torch.equal(out, eager)
         assert torch.equal(run_gpu(other, dev), other_ref)
+
+
+@pytest.mark.parametrize("hq,hkv,b", [(24, 8, 8), (24, 8, 40), (32, 8, 16), (8, 8, 3), (3, 1, 5)])
+def test_fused_rope_decode_equals_separate_ops(dev, hq, hkv, b):
+    """decode_rope_attention (RoPE + KV append + attention in one launch) is
+    bit-identical to rope_kv_store(query_out=...) + paged_attention_decode:
+    output, key cache and value cache.  q/k/v are views into one fused
+    projection row; one position lies outside the RoPE table (not rotated)
+    and one slot is -1 (no store), as the separate ops treat them."""
+    d, bs, mb, rows = 128, 16, 40, 700
+    gen = torch.Generator().manual_seed(hq * 31 + b)
+    ctx = torch.randint(1, mb * bs + 1, (b,), generator=gen).tolist()
+    case = make_decode_case(90 + hq + b, b, ctx, num_heads=hq, num_kv_heads=hkv, max_blocks=mb)
+    pos = torch.tensor([c - 1 for c in ctx], dtype=torch.int32)
+    bt = case.block_tables
+    slots = torch.tensor([int(bt[i, (c - 1) // bs]) * bs + (c - 1) % bs for i, c in enumerate(ctx)],
+                         dtype=torch.int32)
+    if b > 2:
+        slots[1] = -1
+        pos[2] = rows + 5  # outside the table
+    inv = 1.0 / (500000.0 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    ang = torch.outer(torch.arange(rows, dtype=torch.float32), inv)
+    cos, sin = ang.cos().contiguous(), ang.sin().contiguous()
+    qkv = torch.randn(b, (hq + 2 * hkv) * d, generator=gen).half()
+    to = lambda t: t.to(dev)
+    cos_d, sin_d, pos_d, slots_d, bt_d, cl_d = map(to, (cos, sin, pos, slots, bt, case.context_lens))
+
+    def views(buf):
+        return (buf[:, :hq * d].view(b, hq, d), buf[:, hq * d:(hq + hkv) * d].view(b, hkv, d),
+                buf[:, (hq + hkv) * d:].view(b, hkv, d))
+
+    qkv1, kc1, vc1 = to(qkv.clone()), to(case.key_cache.clone()), to(case.value_cache.clone())
+    q1, k1, v1 = views(qkv1)
+    out1 = decode_rope_attention(q1, k1, v1, kc1, vc1, cos_d, sin_d, pos_d, slots_d, bt_d, cl_d,
+                                 mb, case.scale)
+    qkv2, kc2, vc2 = to(qkv.clone()), to(case.key_cache.clone()), to(case.value_cache.clone())
+    q2, k2, v2 = views(qkv2)
+    q_rot = torch.empty(b, hq, d, dtype=torch.float16, device=dev)
+    rope_kv_store(q2, k2, v2, kc2, vc2, cos_d, sin_d, pos_d, slots_d, query_out=q_rot)
+    out2 = ops.paged_attention_decode(q_rot, kc2, vc2, bt_d, cl_d, mb, bs, case.scale)
+    torch.cuda.synchronize()
+    assert torch.equal(qkv1[:, :hq * d], qkv.to(dev)[:, :hq * d])  # query untouched
+    bits = lambda t: t.view(torch.int16)  # the pools hold NaN sentinels
+    assert torch.equal(bits(kc1), bits(kc2)) and torch.equal(bits(vc1), bits(vc2))
+    assert torch.equal(bits(out1), bits(out2))
+
+
+def test_fused_rope_decode_rejects_long_tables(dev):
+    case = make_decode_case(3, 1, [100], max_blocks=128)
+    q = torch.zeros(1, 24, 128, dtype=torch.float16, device=dev)
+    k = torch.zeros(1, 8, 128, dtype=torch.float16, device=dev)
+    tab = torch.zeros(16, 64, device=dev)
+    one = torch.zeros(1, dtype=torch.int32, device=dev)
+    with pytest.raises(RuntimeError, match="capacity"):
+        decode_rope_attention(q, k, k, case.key_cache.to(dev), case.value_cache.to(dev), tab,
+                              tab, one, one, case.block_tables.to(dev), one, 128, 0.1)
 
 
 def test_cfg2_repeat_calls_identical(dev):
