@@ -121,8 +121,17 @@ void prefill_causal_kernel(PrefillArgs a) {
   constexpr int KP = K_PIECES / NT;               // per thread, K and V alike
   static_assert(KP * NT == K_PIECES, "whole tiles per thread");
   constexpr int KS_SIZE = PF_BN * KS_PITCH, VS_SIZE = PF_BN * VS_PITCH;
-  // [key stream][double buffer] K and V tiles; reused for the final merge
-  constexpr int LDS_HALFS = 2 * KSPLIT * (KS_SIZE + VS_SIZE);
+  // Epilogue (reuses the tile buffers): exchanged O halves and (m, l) of the
+  // two key streams, then each wave's finished 32 rows x OUT_DIMS before the
+  // row-contiguous stores (pitch OUT_DIMS + 8 halfs: 16-byte aligned rows).
+  constexpr int OUT_DIMS = PF_HD / KSPLIT;  // dims of a row a wave finishes
+  constexpr int YS_PITCH = OUT_DIMS + 8;
+  constexpr int XCH_FLOATS = KSPLIT == 2 ? 2 * NRB * 32 * 64 : 0;
+  constexpr int ML_FLOATS = KSPLIT == 2 ? 2 * NRB * 2 * 64 : 0;
+  constexpr int EPI_HALFS = 2 * (XCH_FLOATS + ML_FLOATS) + NRB * KSPLIT * 32 * YS_PITCH;
+  // [key stream][double buffer] K and V tiles, then the epilogue buffers
+  constexpr int TILE_HALFS = 2 * KSPLIT * (KS_SIZE + VS_SIZE);
+  constexpr int LDS_HALFS = TILE_HALFS > EPI_HALFS ? TILE_HALFS : EPI_HALFS;
   __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALFS];
   uint16_t *const Ks = lds;
   uint16_t *const Vs = lds + 2 * KSPLIT * KS_SIZE;
@@ -462,60 +471,86 @@ void prefill_causal_kernel(PrefillArgs a) {
     stage_only(u + 1, 1);
   }
 
-  // ---- merge the key streams through LDS (KSPLIT = 2), normalise, store.
-  // Stream 1 publishes (m, l, O) per lane; stream 0 rescales both states to
-  // the larger max, adds them and writes the rows.  O^T is exchanged
-  // register-major (64 lanes x 4 bytes contiguous per register).
-  float m0 = thr > -INFINITY ? m_run : -INFINITY, a0 = 1.f, l_own = l_i;
-  const float *xo = nullptr;
-  float a1 = 0.f;
+  // ---- epilogue: merge the key streams (KSPLIT = 2), normalise, store.
+  // Both streams finish rows: stream kh takes dims OUT_DIMS kh .. +OUT_DIMS-1
+  // of its 32 rows and reads the partner stream's O for those dims, and its
+  // (m, l), from LDS (16-byte lane-major records, conflict-free).  The
+  // finished tile goes through LDS once more so that every store writes whole
+  // rows: OUT_DIMS * 2 bytes of a row by consecutive lanes, 16 bytes each.
+  lds_barrier();  // every wave is done with the K / V^T tiles
+  float *const xo = reinterpret_cast<float *>(lds);  // [kh][rb][8][64 lanes][4]
+  float *const xm = xo + XCH_FLOATS;                 // [kh][rb][2][64 lanes]
+  uint16_t *const ys = reinterpret_cast<uint16_t *>(xm + ML_FLOATS) + w * 32 * YS_PITCH;
+  float s_own, s_oth = 0.f;  // weights of this stream's and the partner's O, 1 / l included
+  const floatx4 *xr = nullptr;
   if constexpr (KSPLIT == 2) {
-    float *xo_w = reinterpret_cast<float *>(lds);  // [NRB][64 registers][64 lanes]
-    float *xm = xo_w + NRB * 64 * 64;              // [NRB][2][64 lanes]
-    static_assert((NRB * 64 * 64 + NRB * 2 * 64) * 4 <= LDS_HALFS * 2,
-                  "merge buffers fit in the staging LDS");
-    lds_barrier();  // every wave is done with the K / V^T tiles
-    if (kh == 1) {
+    const float m_own = thr > -INFINITY ? m_run : -INFINITY;
+    floatx4 *const xw = reinterpret_cast<floatx4 *>(xo) + (kh * NRB + rb) * 8 * 64 + lane;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
+    for (int gq = 0; gq < 8; ++gq) {
+      // the partner's half: o[2 + gq / 4] for stream 0, o[gq / 4] for stream 1
+      // (selects, not an index that depends on kh, keep o in registers)
+      const floatx16 &ox = o[2 + (gq >> 2)], &oy = o[gq >> 2];
+      const int e0 = (gq & 3) * 4;
+      floatx4 x;
 #pragma unroll
-        for (int e = 0; e < 16; ++e) xo_w[(rb * 64 + dt * 16 + e) * 64 + lane] = o[dt][e];
-      xm[(rb * 2 + 0) * 64 + lane] = m0;
-      xm[(rb * 2 + 1) * 64 + lane] = l_i;
+      for (int j = 0; j < 4; ++j) x[j] = kh == 0 ? ox[e0 + j] : oy[e0 + j];
+      xw[gq * 64] = x;
     }
+    xm[((kh * NRB + rb) * 2 + 0) * 64 + lane] = m_own;
+    xm[((kh * NRB + rb) * 2 + 1) * 64 + lane] = l_i;
     lds_barrier();
-    if (kh == 1) return;
+    const int ko = 1 - kh;
+    const float m_oth = xm[((ko * NRB + rb) * 2 + 0) * 64 + lane];
+    const float l_oth = xm[((ko * NRB + rb) * 2 + 1) * 64 + lane];
     // a state that never saw an unmasked key (m = -inf, l = 0, O = 0) gets
-    // weight 0
-    const float m1 = xm[(rb * 2 + 0) * 64 + lane];
-    const float l1 = xm[(rb * 2 + 1) * 64 + lane];
-    const float mm = fmaxf(m0, m1);
-    a0 = fast_exp2(m0 - mm);
-    a1 = fast_exp2(m1 - mm);
-    l_own = l_i * a0 + l1 * a1;
-    xo = xo_w + rb * 64 * 64 + lane;
+    // weight 0; stream 0 always sees key 0, so mm is finite on real rows
+    const float mm = fmaxf(m_own, m_oth);
+    const float a_own = fast_exp2(m_own - mm), a_oth = fast_exp2(m_oth - mm);
+    const float inv = 1.0f / xor32_add(l_i * a_own + l_oth * a_oth);
+    s_own = a_own * inv;
+    s_oth = a_oth * inv;
+    xr = reinterpret_cast<const floatx4 *>(xo) + (ko * NRB + rb) * 8 * 64 + lane;
+  } else {
+    s_own = 1.0f / xor32_add(l_i);
   }
-  const float l_tot = xor32_add(l_own);
-  if (row_ok) {
-    const float inv = 1.0f / l_tot;
-    const float s0 = a0 * inv, s1 = a1 * inv;
-    uint16_t *op = a.out + ((int64_t)b * S + pos) * q_row_stride + (int64_t)h * PF_HD + 4 * hf;
+  // lane: row r32 of the wave, dims 32 dd + 8 e4 + 4 hf + 0..3 of its half
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+  for (int dd = 0; dd < OUT_DIMS / 32; ++dd)
 #pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        float v[4];
+    for (int e4 = 0; e4 < 4; ++e4) {
+      floatx4 x = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (KSPLIT == 2) x = xr[(dd * 4 + e4) * 64];
+      float v[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int e = 4 * e4 + j;
-          v[j] = o[dt][e] * s0;
-          if constexpr (KSPLIT == 2) v[j] += xo[(dt * 16 + e) * 64] * s1;
-        }
-        u32x2 pr;
-        pr[0] = pack2<T>(v[0], v[1]);
-        pr[1] = pack2<T>(v[2], v[3]);
-        *reinterpret_cast<u32x2 *>(op + dt * 32 + 8 * e4) = pr;
+      for (int j = 0; j < 4; ++j) {
+        const int e = 4 * e4 + j;
+        const float own = KSPLIT == 2 ? (kh == 0 ? o[dd][e] : o[2 + dd][e]) : o[dd][e];
+        v[j] = own * s_own + x[j] * s_oth;
       }
+      u32x2 pr;
+      pr[0] = pack2<T>(v[0], v[1]);
+      pr[1] = pack2<T>(v[2], v[3]);
+      *reinterpret_cast<u32x2 *>(&ys[r32 * YS_PITCH + dd * 32 + 8 * e4 + 4 * hf]) = pr;
+    }
+  // the wave reads back rows written by its other lanes: LDS operations of a
+  // wave complete in order, so only the compiler has to keep the order
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+  constexpr int CH = OUT_DIMS / 8;  // 16-byte chunks per row
+  constexpr int RPI = 64 / CH;      // rows per store instruction
+  const int dim0 = KSPLIT == 2 ? OUT_DIMS * kh : 0;
+#pragma unroll
+  for (int i = 0; i < 32 / RPI; ++i) {
+    const int rr = i * RPI + lane / CH, ch = lane % CH;
+    const u32x4 val = *reinterpret_cast<const u32x4 *>(&ys[rr * YS_PITCH + 8 * ch]);
+    const int grow = r_wave + rr;
+    if (grow < rows_total) {
+      const int p = grow / G, hh = g * G + (grow - p * G);
+      *reinterpret_cast<u32x4 *>(a.out + ((int64_t)b * S + p) * q_row_stride +
+                                 (int64_t)hh * PF_HD + dim0 + 8 * ch) = val;
+    }
   }
 }
 
