@@ -211,14 +211,30 @@ MCE_API int mce_rope_kv_store(int dtype, void *query, void *query_out, void *key
  *   MCE_EPI_SWIGLU w is [2n, k] (gate rows, then up rows);
  *                  out[:, j] = silu(x w_gate_j) * (x w_up_j)
  * x rows x_stride elements apart, out rows out_stride apart.  Needs
- * n % 16 == 0, k a multiple of 512 with k / 512 <= 16 (<= 8 for SwiGLU);
- * other shapes return MCE_ERR_UNSUPPORTED (callers then use a library GEMM).
+ * n % 16 == 0 and k in {2048, 3072, 4096}, or k == 8192 for m <= 8 without
+ * SwiGLU; other shapes return MCE_ERR_UNSUPPORTED (callers then use a library
+ * GEMM).
  * No single counterpart in the reference: its decode step runs these
  * projections through torch.matmul, then a separate SwiGLU kernel and
  * residual adds (engine/models/llama.py:94-110,143-165,174).
  */
 MCE_API int mce_decode_gemm(int dtype, const void *x, const void *w, void *out, int m, int n,
                     int k, int64_t x_stride, int64_t out_stride, int epilogue, void *stream);
+
+/*
+ * RMSNorm fused in front of mce_decode_gemm: out (op)= rmsnorm(x) w^T with
+ * rmsnorm(x)[m, :] = x[m, :] / sqrt(mean(x[m, :]^2) + eps) * norm_weight
+ * (norm_weight [k]), the normalised rows bit-identical to mce_rmsnorm's
+ * output; same epilogues, layouts and shape rules as mce_decode_gemm, k in
+ * {2048, 3072, 4096}.  The normalised rows are not written out.  Replaces the
+ * RMSNorm + projection pairs of the reference decode step
+ * (engine/models/llama.py:104-110 input_layernorm + q/k/v, :143-147
+ * post_attention_layernorm + gate/up, with csrc/kernels/rmsnorm.cu:35-130).
+ */
+MCE_API int mce_rmsnorm_decode_gemm(int dtype, const void *x, const void *norm_weight, float eps,
+                                    const void *w, void *out, int m, int n, int k,
+                                    int64_t x_stride, int64_t out_stride, int epilogue,
+                                    void *stream);
 
 /*
  * Causal prefill attention over contiguous Q/K/V, GQA:

@@ -1,85 +1,174 @@
-// Decode-sized GEMM for gfx950: out[M, N] (op)= X[M, K] . W[N, K]^T with
-// M <= 16 (one token per sequence), fp16 in, fp32 accumulation, fused
-// epilogues.  This is the projection work of the engine's decode step
-// (engine/models/llama.py:94-174 runs it through torch.matmul); at these
-// shapes it is a weight-streaming problem: every W byte is read once and
-// the MFMA work is negligible.
+// Decode-sized GEMM for gfx950: out[M, N] (op)= xn[M, K] . W[N, K]^T with
+// M <= 16 (one token per sequence), fp16 in, fp32 accumulation; xn is x or
+// RMSNorm(x) (fused in front), and the epilogue stores, adds into the
+// residual stream or applies SwiGLU.  This is the projection work of the
+// engine's decode step (engine/models/llama.py:94-174 runs it through
+// torch.matmul with separate RMSNorm and SwiGLU kernels); at these shapes it
+// is a weight-streaming problem: every W byte is read once and the MFMA work
+// is negligible.
 //
-// Layout of one launch:
-//   * a workgroup owns 16 output columns (16 rows of W) -- two 16-row tiles
-//     for the SwiGLU epilogue (gate rows j and up rows n + j) -- and has one
-//     wave per 512-wide slice of K per tile;
-//   * a wave issues all 16 of its W loads (16 rows x 64 bytes per instruction,
-//     consecutive instructions covering consecutive 64-byte halves of the same
-//     128-byte lines) and its X loads (L2-resident) up front, then runs 16
-//     v_mfma_f32_16x16x32_f16: A = W tile (lane l: row l % 16, k 8 (l / 16)
-//     .. +7), B = X^T (lane l: token l % 16, same k); tokens >= M are zeros;
-//   * the K-slice partials (4 floats per lane: rows 4 (l / 16) .. +3, token
-//     l % 16) are summed through LDS and the first wave applies the epilogue.
-// Epilogues: STORE  out[m, n] = acc
-//            ADD    out[m, n] = out[m, n] + acc   (residual stream in place)
-//            SWIGLU out[m, j] = silu(acc_gate[m, j]) * acc_up[m, j], W being
-//                   [2 n, K] with the gate rows first (the fused gate/up
-//                   weight), so one launch replaces GEMM + SwiGLU.
+// Layout of one launch (grid = N / 16 workgroups of 8 waves):
+//   * a workgroup owns 16 output columns (16 rows of W; gate rows j and up
+//     rows n + j for SwiGLU); wave w takes the K slice [w K / 8, (w + 1) K / 8)
+//     as C = K / 256 chunks of 32;
+//   * x (normalised when fused) is staged once per workgroup in LDS as the
+//     MFMA B operand: 16-byte groups of 8 consecutive k, [k / 8][token slot],
+//     the slot XOR-swizzled by the group index so that the staging writes (a
+//     wave per token, consecutive groups) and the fragment reads (the tokens
+//     of one group) both hit 16 different 16-byte bank groups;
+//   * W fragments (A operand: lane l holds row l % 16, k 8 (l / 16) .. +7) go
+//     from HBM straight into registers: the x loads are issued first (loads
+//     return in order, so staging x waits for x only), then the first half of
+//     the W fragments, then x is staged and the second half issued.  Register
+//     use stays low enough for every workgroup of a launch to be resident, so
+//     the whole weight is in flight at once;
+//   * one v_mfma_f32_16x16x32_f16 per chunk and tile (tokens >= M are zeros);
+//     the 8 K-slice partials (lane l: rows 4 (l / 16) .. +3, token l % 16)
+//     are summed in LDS and wave 0 applies the epilogue:
+//       STORE  out[m, n] = acc
+//       ADD    out[m, n] = out[m, n] + acc          (residual stream, in place)
+//       SWIGLU out[m, j] = silu(acc_gate) * acc_up  (W = [2 n, K], gate rows first)
+// The fused RMSNorm computes each token's scale exactly as mce_rmsnorm does
+// (same per-lane chunk order, reduction and rounding), so xn is bit-identical
+// to that op's output.
 #include "mce_common.h"
 
 namespace mce {
 
-constexpr int DG_SLICE = 512;       // K per wave
-constexpr int DG_CHUNKS = DG_SLICE / 32;
-constexpr int DG_MAX_WAVES = 16;    // per workgroup (1024 threads)
+constexpr int DG_WAVES = 8;
 
 struct DecodeGemmArgs {
-  const uint16_t *x, *w;
+  const uint16_t *x, *w, *norm_w;
   uint16_t *out;
-  int M, N, K;
+  int M, N;
   int64_t x_stride, out_stride;
+  float eps;
 };
 
-template <int EPI, int T>  // T tiles per workgroup (2 for SWIGLU)
-__global__ __launch_bounds__(DG_MAX_WAVES * 64) void decode_gemm_kernel(DecodeGemmArgs a) {
-  const int nw = a.K / DG_SLICE;  // waves per tile
+// 16-byte group index of k group kg, token slot t in the staged x
+template <int MP>
+__device__ __forceinline__ int xs_group(int kg, int t) {
+  if constexpr (MP == 16)
+    return kg * 16 + (t ^ (kg & 15));
+  else
+    return kg * 8 + (t ^ ((kg >> 1) & 7));
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  return g / (1.0f + __expf(-g)) * u;
+}
+
+// EPI: 0 store, 1 add, 2 SwiGLU; TT tiles per workgroup (2 for SwiGLU);
+// MP token slots (8 or 16); NORM: fuse RMSNorm; C chunks of 32 k per wave.
+template <int EPI, int TT, int MP, bool NORM, int C, int WPE>
+__global__ __launch_bounds__(DG_WAVES * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
+void decode_gemm_kernel(DecodeGemmArgs a) {
+  constexpr int K = C * 256;
+  constexpr int VPT = K / 512;      // 16-byte groups of one token row per lane
+  constexpr int NTOK = MP / 8;      // token rows staged per wave
+  constexpr int C1 = (C + 1) / 2;   // W chunks fetched before x is staged
+  __shared__ __attribute__((aligned(16))) uint16_t xs[K / 8 * MP * 8];
+  static_assert(K / 8 * MP * 8 * 2 >= DG_WAVES * TT * 4 * 64 * 4, "reduction fits");
+
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tile = wave / nw, slice = wave - tile * nw;
-  const int col0 = blockIdx.x * 16;                   // first output column
-  const int wrow0 = col0 + tile * a.N;                // first W row of this tile
+  const int col0 = blockIdx.x * 16;
   const int r = lane & 15, q = lane >> 4;
-  const int k0 = slice * DG_SLICE + 8 * q;
 
-  // all loads of the wave first: 16 W fragments (HBM) and 16 X fragments
-  const uint16_t *wp = a.w + (int64_t)(wrow0 + r) * a.K + k0;
-  const bool tok_ok = r < a.M;
-  const uint16_t *xp = a.x + (int64_t)(tok_ok ? r : 0) * a.x_stride + k0;
-  u32x4 wf[DG_CHUNKS], xf[DG_CHUNKS];
+  // 1. this wave's token rows of x (and the norm weights)
+  u32x4 xv[NTOK][VPT];
+  u32x4 nw[NORM ? VPT : 1];
 #pragma unroll
-  for (int c = 0; c < DG_CHUNKS; ++c)
-    wf[c] = *reinterpret_cast<const u32x4 *>(wp + 32 * c);
+  for (int j = 0; j < NTOK; ++j) {
+    const int m = wave + 8 * j;
+    if (m < a.M) {
+      const uint16_t *xr = a.x + (int64_t)m * a.x_stride;
 #pragma unroll
-  for (int c = 0; c < DG_CHUNKS; ++c)
-    xf[c] = tok_ok ? *reinterpret_cast<const u32x4 *>(xp + 32 * c) : u32x4{0, 0, 0, 0};
-  floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < VPT; ++i)
+        xv[j][i] = *reinterpret_cast<const u32x4 *>(xr + (lane + 64 * i) * 8);
+    }
+  }
+  if constexpr (NORM) {
 #pragma unroll
-  for (int c = 0; c < DG_CHUNKS; ++c)
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wf[c]),
-                                                 __builtin_bit_cast(half8, xf[c]), acc, 0, 0, 0);
+    for (int i = 0; i < VPT; ++i)
+      nw[i] = *reinterpret_cast<const u32x4 *>(a.norm_w + (lane + 64 * i) * 8);
+  }
 
-  // sum the K slices: red[wave][component][lane]
-  __shared__ float red[DG_MAX_WAVES][4][64];
+  // 2. first half of the W fragments
+  const uint16_t *wp[TT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) red[wave][i][lane] = acc[i];
+  for (int t = 0; t < TT; ++t)
+    wp[t] = a.w + (int64_t)(col0 + t * a.N + r) * K + wave * (K / 8) + 8 * q;
+  u32x4 wf[TT][C];
+#pragma unroll
+  for (int c = 0; c < C1; ++c)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) wf[t][c] = *reinterpret_cast<const u32x4 *>(wp[t] + 32 * c);
+
+  // 3. stage x (normalised) into LDS; slots of tokens >= M hold zeros
+#pragma unroll
+  for (int j = 0; j < NTOK; ++j) {
+    const int m = wave + 8 * j;
+    if (m < a.M) {
+      float inv = 1.0f;
+      if constexpr (NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) ss = sumsq8<F16T>(xv[j][i], ss);
+        inv = rms_inv(wave_sum(ss), K, a.eps);
+      }
+#pragma unroll
+      for (int i = 0; i < VPT; ++i) {
+        const u32x4 val = NORM ? rms_scale8<F16T>(xv[j][i], nw[NORM ? i : 0], inv) : xv[j][i];
+        *reinterpret_cast<u32x4 *>(&xs[xs_group<MP>(lane + 64 * i, m) * 8]) = val;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+        *reinterpret_cast<u32x4 *>(&xs[xs_group<MP>(lane + 64 * i, m) * 8]) = u32x4{0, 0, 0, 0};
+    }
+  }
+
+  // 4. second half of the W fragments, then the MFMAs
+#pragma unroll
+  for (int c = C1; c < C; ++c)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) wf[t][c] = *reinterpret_cast<const u32x4 *>(wp[t] + 32 * c);
   lds_barrier();
-  if (wave != 0) return;
-  float v[T][4];
+  floatx4 acc[TT];
 #pragma unroll
-  for (int t = 0; t < T; ++t)
+  for (int t = 0; t < TT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int kg = (wave * C + c) * 4 + q;
+    u32x4 xf = *reinterpret_cast<const u32x4 *>(&xs[xs_group<MP>(kg, r & (MP - 1)) * 8]);
+    if constexpr (MP == 8) xf = r < 8 ? xf : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+      acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, wf[t][c]),
+                                                      __builtin_bit_cast(half8, xf), acc[t], 0, 0,
+                                                      0);
+  }
+
+  // 5. sum the K slices: red[wave][tile][component][lane]
+  lds_barrier();  // every wave is done reading xs
+  float *const red = reinterpret_cast<float *>(xs);
+#pragma unroll
+  for (int t = 0; t < TT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[((wave * TT + t) * 4 + i) * 64 + lane] = acc[t][i];
+  lds_barrier();
+  if (wave != 0 || r >= a.M) return;
+  float v[TT][4];
+#pragma unroll
+  for (int t = 0; t < TT; ++t)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float s = 0.f;
-      for (int sl = 0; sl < nw; ++sl) s += red[t * nw + sl][i][lane];
+#pragma unroll
+      for (int sl = 0; sl < DG_WAVES; ++sl) s += red[((sl * TT + t) * 4 + i) * 64 + lane];
       v[t][i] = s;
     }
-  if (!tok_ok) return;
   // lane holds columns col0 + 4 q .. +3 of token r
   uint16_t *op = a.out + (int64_t)r * a.out_stride + col0 + 4 * q;
   float o[4];
@@ -91,10 +180,7 @@ __global__ __launch_bounds__(DG_MAX_WAVES * 64) void decode_gemm_kernel(DecodeGe
     o[3] = F16T::hi(old[1]) + v[0][3];
   } else if constexpr (EPI == 2) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float g = v[0][i];
-      o[i] = g / (1.0f + __expf(-g)) * v[T - 1][i];
-    }
+    for (int i = 0; i < 4; ++i) o[i] = silu_mul(v[0][i], v[TT - 1][i]);
   } else {
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = v[0][i];
@@ -105,6 +191,82 @@ __global__ __launch_bounds__(DG_MAX_WAVES * 64) void decode_gemm_kernel(DecodeGe
   *reinterpret_cast<u32x2 *>(op) = pr;
 }
 
+template <int EPI, int TT, int MP, bool NORM, int C>
+void launch_dg(const DecodeGemmArgs &a, hipStream_t st) {
+  // registers of the W fragments decide how many waves fit per SIMD; every
+  // workgroup of a launch should be resident at once
+  constexpr int WPE = TT * C <= 24 && MP == 8 ? 4 : 2;
+  decode_gemm_kernel<EPI, TT, MP, NORM, C, WPE><<<a.N / 16, DG_WAVES * 64, 0, st>>>(a);
+}
+
+template <int EPI, int TT, int MP, bool NORM>
+int dispatch_k(const DecodeGemmArgs &a, int k, hipStream_t st) {
+  switch (k) {
+    case 2048: launch_dg<EPI, TT, MP, NORM, 8>(a, st); return MCE_OK;
+    case 3072: launch_dg<EPI, TT, MP, NORM, 12>(a, st); return MCE_OK;
+    case 4096: launch_dg<EPI, TT, MP, NORM, 16>(a, st); return MCE_OK;
+    case 8192:
+      if constexpr (TT == 1 && !NORM && MP == 8) {  // 128 KB of staged x
+        launch_dg<EPI, TT, MP, NORM, 32>(a, st);
+        return MCE_OK;
+      }
+      break;
+  }
+  return MCE_ERR_UNSUPPORTED;
+}
+
+template <bool NORM>
+int dispatch(const DecodeGemmArgs &a, int k, int epilogue, hipStream_t st) {
+  const bool small = a.M <= 8;
+  if (epilogue == MCE_EPI_STORE)
+    return small ? dispatch_k<0, 1, 8, NORM>(a, k, st) : dispatch_k<0, 1, 16, NORM>(a, k, st);
+  if (epilogue == MCE_EPI_ADD)
+    return small ? dispatch_k<1, 1, 8, NORM>(a, k, st) : dispatch_k<1, 1, 16, NORM>(a, k, st);
+  return small ? dispatch_k<2, 2, 8, NORM>(a, k, st) : dispatch_k<2, 2, 16, NORM>(a, k, st);
+}
+
+int decode_gemm_impl(const char *name, int dtype, const void *x, const void *norm_w, float eps,
+                     const void *w, void *out, int m, int n, int k, int64_t x_stride,
+                     int64_t out_stride, int epilogue, void *stream) {
+  clear_error();
+  MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16, "%s: unknown dtype %d", name, dtype);
+  if (dtype != MCE_F16) return set_error(MCE_ERR_UNSUPPORTED, "%s: only fp16 is implemented", name);
+  MCE_REQUIRE(epilogue >= MCE_EPI_STORE && epilogue <= MCE_EPI_SWIGLU, "%s: unknown epilogue %d",
+              name, epilogue);
+  MCE_REQUIRE(m >= 0 && n >= 0 && k >= 0, "%s: bad shape", name);
+  if (m == 0 || n == 0) return MCE_OK;
+  const bool norm = norm_w != nullptr;
+  const bool k_ok = k == 2048 || k == 3072 || k == 4096 ||
+                    (k == 8192 && !norm && epilogue != MCE_EPI_SWIGLU && m <= 8);
+  if (m > 16 || n % 16 != 0 || !k_ok)
+    return set_error(MCE_ERR_UNSUPPORTED,
+                     "%s: needs m <= 16, n %% 16 == 0 and k in {2048, 3072, 4096} (8192 for m <= 8 "
+                     "without the fused RMSNorm or SwiGLU) (got m=%d n=%d k=%d)",
+                     name, m, n, k);
+  MCE_REQUIRE(x && w && out, "%s: null pointer", name);
+  MCE_REQUIRE(x_stride >= k && x_stride % 8 == 0 && out_stride >= n && out_stride % 4 == 0,
+              "%s: bad row strides", name);
+  MCE_REQUIRE(aligned16(x) && aligned16(w) && (!norm || aligned16(norm_w)) &&
+                  (reinterpret_cast<uintptr_t>(out) & 7) == 0,
+              "%s: x, w and the norm weight must be 16-byte aligned, out 8-byte aligned", name);
+  MCE_REQUIRE((int64_t)n * k * (epilogue == MCE_EPI_SWIGLU ? 2 : 1) < ((int64_t)1 << 31),
+              "%s: weight too large", name);
+  DecodeGemmArgs a{};
+  a.x = (const uint16_t *)x;
+  a.w = (const uint16_t *)w;
+  a.norm_w = (const uint16_t *)norm_w;
+  a.out = (uint16_t *)out;
+  a.M = m;
+  a.N = n;
+  a.x_stride = x_stride;
+  a.out_stride = out_stride;
+  a.eps = eps;
+  hipStream_t st = (hipStream_t)stream;
+  const int rc = norm ? dispatch<true>(a, k, epilogue, st) : dispatch<false>(a, k, epilogue, st);
+  if (rc != MCE_OK) return set_error(rc, "%s: no kernel for k=%d", name, k);
+  return check_launch(name);
+}
+
 }  // namespace mce
 
 using namespace mce;
@@ -112,44 +274,17 @@ using namespace mce;
 extern "C" int mce_decode_gemm(int dtype, const void *x, const void *w, void *out, int m, int n,
                                int k, int64_t x_stride, int64_t out_stride, int epilogue,
                                void *stream) {
+  return decode_gemm_impl("mce_decode_gemm", dtype, x, nullptr, 0.f, w, out, m, n, k, x_stride,
+                          out_stride, epilogue, stream);
+}
+
+extern "C" int mce_rmsnorm_decode_gemm(int dtype, const void *x, const void *norm_weight,
+                                       float eps, const void *w, void *out, int m, int n, int k,
+                                       int64_t x_stride, int64_t out_stride, int epilogue,
+                                       void *stream) {
   clear_error();
-  MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16, "mce_decode_gemm: unknown dtype %d", dtype);
-  if (dtype != MCE_F16)
-    return set_error(MCE_ERR_UNSUPPORTED, "mce_decode_gemm: only fp16 is implemented");
-  MCE_REQUIRE(epilogue >= MCE_EPI_STORE && epilogue <= MCE_EPI_SWIGLU,
-              "mce_decode_gemm: unknown epilogue %d", epilogue);
-  MCE_REQUIRE(m >= 0 && n >= 0 && k >= 0, "mce_decode_gemm: bad shape");
-  if (m == 0 || n == 0) return MCE_OK;
-  if (m > 16 || n % 16 != 0 || k % DG_SLICE != 0 || k == 0 ||
-      k / DG_SLICE * (epilogue == MCE_EPI_SWIGLU ? 2 : 1) > DG_MAX_WAVES)
-    return set_error(MCE_ERR_UNSUPPORTED,
-                     "mce_decode_gemm: needs m <= 16, n %% 16 == 0, k a multiple of %d with "
-                     "k / %d (x2 for SwiGLU) <= %d waves (got m=%d n=%d k=%d)",
-                     DG_SLICE, DG_SLICE, DG_MAX_WAVES, m, n, k);
-  MCE_REQUIRE(x && w && out, "mce_decode_gemm: null pointer");
-  MCE_REQUIRE(x_stride >= k && x_stride % 8 == 0 && out_stride >= n && out_stride % 4 == 0,
-              "mce_decode_gemm: bad row strides");
-  MCE_REQUIRE(aligned16(x) && aligned16(w) && (reinterpret_cast<uintptr_t>(out) & 7) == 0,
-              "mce_decode_gemm: x and w must be 16-byte aligned, out 8-byte aligned");
-  MCE_REQUIRE((int64_t)n * k * (epilogue == MCE_EPI_SWIGLU ? 2 : 1) < ((int64_t)1 << 31),
-              "mce_decode_gemm: weight too large");
-  DecodeGemmArgs a{};
-  a.x = (const uint16_t *)x;
-  a.w = (const uint16_t *)w;
-  a.out = (uint16_t *)out;
-  a.M = m;
-  a.N = n;
-  a.K = k;
-  a.x_stride = x_stride;
-  a.out_stride = out_stride;
-  hipStream_t st = (hipStream_t)stream;
-  const int nw = k / DG_SLICE;
-  const dim3 grid(n / 16);
-  if (epilogue == MCE_EPI_STORE)
-    decode_gemm_kernel<0, 1><<<grid, nw * 64, 0, st>>>(a);
-  else if (epilogue == MCE_EPI_ADD)
-    decode_gemm_kernel<1, 1><<<grid, nw * 64, 0, st>>>(a);
-  else
-    decode_gemm_kernel<2, 2><<<grid, 2 * nw * 64, 0, st>>>(a);
-  return check_launch("mce_decode_gemm");
+  MCE_REQUIRE(norm_weight != nullptr, "mce_rmsnorm_decode_gemm: null norm weight");
+  MCE_REQUIRE(eps >= 0.f, "mce_rmsnorm_decode_gemm: eps must be >= 0");
+  return decode_gemm_impl("mce_rmsnorm_decode_gemm", dtype, x, norm_weight, eps, w, out, m, n, k,
+                          x_stride, out_stride, epilogue, stream);
 }

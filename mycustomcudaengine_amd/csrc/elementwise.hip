@@ -40,29 +40,16 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(
     int idx = lane + i * 64;
     if (idx < nvec) {
       v[i] = xr[idx];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        float a = T::lo(v[i][k]), b = T::hi(v[i][k]);
-        ss += a * a + b * b;
-      }
+      ss = sumsq8<T>(v[i], ss);
     }
   }
   ss = wave_sum(ss);
-  const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
+  const float inv = rms_inv(ss, hidden, eps);
   u32x4 *yr = reinterpret_cast<u32x4 *>(y + row * out_stride);
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     int idx = lane + i * 64;
-    if (idx < nvec) {
-      u32x4 o;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        float a = T::lo(v[i][k]) * (inv * T::lo(wv[i][k]));
-        float b = T::hi(v[i][k]) * (inv * T::hi(wv[i][k]));
-        o[k] = pack2<T>(a, b);
-      }
-      yr[idx] = o;
-    }
+    if (idx < nvec) yr[idx] = rms_scale8<T>(v[i], wv[i], inv);
   }
 }
 

@@ -165,6 +165,37 @@ __device__ inline void rope_pair(float x0, float x1, float c, float s, float &r0
   r1 = x0 * s + x1 * c;
 }
 
+// RMSNorm pieces shared by every kernel that normalises rows, so that they
+// all round identically: the sum of squares of a 16-byte chunk accumulated
+// in a fixed order with explicit FMAs, and y = x * (inv_rms * w).
+template <class T>
+__device__ inline float sumsq8(const u32x4 &v, float ss) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float a = T::lo(v[k]), b = T::hi(v[k]);
+    ss = __builtin_fmaf(a, a, ss);
+    ss = __builtin_fmaf(b, b, ss);
+  }
+  return ss;
+}
+
+template <class T>
+__device__ inline u32x4 rms_scale8(const u32x4 &v, const u32x4 &w, float inv) {
+  u32x4 o;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float a = T::lo(v[k]) * (inv * T::lo(w[k]));
+    const float b = T::hi(v[k]) * (inv * T::hi(w[k]));
+    o[k] = pack2<T>(a, b);
+  }
+  return o;
+}
+
+// 1 / sqrt(mean of squares + eps), the RMSNorm row scale.
+__device__ inline float rms_inv(float ss, int hidden, float eps) {
+  return 1.0f / sqrtf(ss / (float)hidden + eps);
+}
+
 // Workgroup barrier that orders LDS accesses only.  The fences are scoped to
 // the local (LDS) address space, so the wait before s_barrier covers this
 // wave's LDS operations (lgkmcnt) while global loads issued earlier stay in

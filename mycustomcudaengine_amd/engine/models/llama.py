@@ -24,7 +24,13 @@ q and k, writes k/v to their pages and runs the attention
 a contiguous buffer) and k and writes k/v to their pages, then the decode
 attention runs (the reference calls rope_inplace, paged_kv_store and
 paged_attention_decode, llama.py:117-134).  The o_proj / down_proj GEMMs add
-into the residual stream in place (addmm_) instead of a separate add.
+into the residual stream in place instead of a separate add.  At decode
+batch sizes (at most 8 tokens, fp16, the 3B model's widths) the projections
+run on the decode-sized GEMM kernels: RMSNorm fused in front of the q/k/v and
+gate/up projections, SwiGLU fused behind gate/up, the residual adds fused
+into o_proj / down_proj, the final RMSNorm in front of lm_head -- 4 launches
+per layer besides the attention instead of 7; other shapes use torch.matmul
+(hipBLASLt) with the separate RMSNorm / SwiGLU ops.
 RoPE tables cover max_position_embeddings positions (capped at 131072)
 instead of the reference's fixed 4096 (llama.py:42).
 """
@@ -37,7 +43,8 @@ import torch
 
 import my_cuda_engine_cpp as ops
 
-from ...ops import PER_SEQ_MAX_TOKENS, decode_rope_attention, rope_kv_store
+from ...ops import (PER_SEQ_MAX_TOKENS, decode_gemm, decode_rope_attention, rmsnorm_decode_gemm,
+                   rope_kv_store)
 from ..cache import KVCacheManager
 
 ROPE_TABLE_CAP = 131072
@@ -76,6 +83,7 @@ class Llama3BEngineModel:
         self.scale = 1.0 / math.sqrt(config.head_dim)
         emb = weights["model.embed_tokens.weight"]
         self.device = emb.device
+        self.dtype = emb.dtype
         n = rope_positions or min(config.max_position_embeddings, ROPE_TABLE_CAP)
         self.cos_table, self.sin_table = rope_tables(n, config.head_dim, config.rope_theta,
                                                      self.device)
@@ -123,6 +131,19 @@ class Llama3BEngineModel:
         act = ops.swiglu(torch.matmul(xn, self.w_gate_up[l].T))
         x.addmm_(act, self.weights[f"{p}.mlp.down_proj.weight"].T)
 
+    def _decode_gemms_take(self, b: int) -> bool:
+        """Whether the decode-sized GEMM kernels take every projection of a
+        decode step of b tokens: fp16, b <= 8 (the down projection stages its
+        whole K = intermediate-size rows), K in {2048, 3072, 4096} (8192 for
+        down_proj), every N a multiple of 16."""
+        c = self.config
+        ks = {2048, 3072, 4096}
+        hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+        return (self.dtype == torch.float16 and 1 <= b <= 8 and c.hidden_size in ks and
+                hq * d in ks and c.intermediate_size in ks | {8192} and
+                all(n % 16 == 0 for n in ((hq + 2 * hkv) * d, c.hidden_size,
+                                          c.intermediate_size, self.lm_head.shape[0])))
+
     def decode_step(self, input_ids: torch.Tensor, positions: torch.Tensor,
                     context_lens: torch.Tensor, slot_mapping: torch.Tensor,
                     block_tables_tensor: torch.Tensor, max_blocks_per_seq: int) -> torch.Tensor:
@@ -134,10 +155,16 @@ class Llama3BEngineModel:
         kv = self.cache_manager.kv_cache
         # tables of at most PER_SEQ_MAX_TOKENS: RoPE + KV append fused into attention
         fused = max_blocks_per_seq * self.cache_manager.block_size <= PER_SEQ_MAX_TOKENS
+        gemms = self._decode_gemms_take(b)
+        eps = c.rms_norm_eps
         for l in range(c.num_hidden_layers):
             p = f"model.layers.{l}"
-            xn = ops.rmsnorm(x, self.weights[f"{p}.input_layernorm.weight"], c.rms_norm_eps)
-            q, k, v = self._attention_block_proj(l, xn)
+            ln_in = self.weights[f"{p}.input_layernorm.weight"]
+            if gemms:  # RMSNorm + q/k/v projection in one launch
+                qkv = rmsnorm_decode_gemm(x, ln_in, eps, self.w_qkv[l])
+                q, k, v = qkv[:, : hq * d], qkv[:, hq * d:(hq + hkv) * d], qkv[:, (hq + hkv) * d:]
+            else:
+                q, k, v = self._attention_block_proj(l, ops.rmsnorm(x, ln_in, eps))
             q3, k3, v3 = q.view(b, hq, d), k.view(b, hkv, d), v.view(b, hkv, d)
             if fused:  # RoPE, KV append and attention in one launch
                 attn = decode_rope_attention(q3, k3, v3, kv[l, 0], kv[l, 1], self.cos_table,
@@ -152,7 +179,17 @@ class Llama3BEngineModel:
                                                   block_tables_tensor, context_lens,
                                                   max_blocks_per_seq,
                                                   self.cache_manager.block_size, self.scale)
-            x.addmm_(attn.view(b, hq * d), self.weights[f"{p}.self_attn.o_proj.weight"].T)
-            self._mlp(l, x)
-        xf = ops.rmsnorm(x, self.weights["model.norm.weight"], c.rms_norm_eps)
+            w_o = self.weights[f"{p}.self_attn.o_proj.weight"]
+            if gemms:  # o_proj + residual; RMSNorm + gate/up + SwiGLU; down_proj + residual
+                decode_gemm(attn.view(b, hq * d), w_o, out=x, epilogue="add")
+                act = rmsnorm_decode_gemm(x, self.weights[f"{p}.post_attention_layernorm.weight"],
+                                          eps, self.w_gate_up[l], epilogue="swiglu")
+                decode_gemm(act, self.weights[f"{p}.mlp.down_proj.weight"], out=x,
+                            epilogue="add")
+            else:
+                x.addmm_(attn.view(b, hq * d), w_o.T)
+                self._mlp(l, x)
+        if gemms:
+            return rmsnorm_decode_gemm(x, self.weights["model.norm.weight"], eps, self.lm_head)
+        xf = ops.rmsnorm(x, self.weights["model.norm.weight"], eps)
         return torch.matmul(xf, self.lm_head.T)

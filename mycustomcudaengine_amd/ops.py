@@ -358,6 +358,31 @@ def decode_rope_attention(query: torch.Tensor, key: torch.Tensor, value: torch.T
 _EPILOGUES = {"store": 0, "add": 1, "swiglu": 2}
 
 
+def _projection(name: str, x: torch.Tensor, weight: torch.Tensor, out, epilogue: str):
+    """Shared argument checks of the decode-sized projections; returns
+    (device, dtype code, m, n, k, out)."""
+    dev = _on_gpu(name, x, weight)
+    code = _dtype_code(x, f"{name} x")
+    _check(weight.dtype == x.dtype, f"{name}: weight dtype must match x")
+    _check(x.dim() == 2 and weight.dim() == 2 and x.size(1) == weight.size(1),
+           f"{name}: x [M, K] and weight [N, K] expected (got {tuple(x.shape)}, "
+           f"{tuple(weight.shape)})")
+    _check(epilogue in _EPILOGUES, f"{name}: unknown epilogue {epilogue!r}")
+    _check(x.stride(1) == 1 and weight.is_contiguous(),
+           f"{name}: x last dim and weight must be contiguous")
+    m, k = x.shape
+    n = weight.size(0) // 2 if epilogue == "swiglu" else weight.size(0)
+    _check(epilogue != "swiglu" or weight.size(0) % 2 == 0,
+           f"{name}: swiglu weight needs an even number of rows")
+    if out is None:
+        _check(epilogue != "add", f"{name}: epilogue 'add' needs out")
+        out = torch.empty(m, n, dtype=x.dtype, device=x.device)
+    _check(out.dtype == x.dtype and out.dim() == 2 and tuple(out.shape) == (m, n) and
+           out.stride(1) == 1 and out.device == x.device,
+           f"{name}: out must be [{m}, {n}] with a contiguous last dim")
+    return dev, code, m, n, k, out
+
+
 def decode_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None,
                 epilogue: str = "store") -> torch.Tensor:
     """Decode-sized projection out (op)= x . weight^T for at most 16 rows.
@@ -367,32 +392,33 @@ def decode_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None,
     writes a new (or the given) [M, N] tensor; "add" accumulates into `out`
     in place (residual stream); "swiglu" returns silu(x W_gate^T) * x W_up^T.
     Raises MCEError with code MCE_ERR_UNSUPPORTED for shapes the kernel does
-    not take (M > 16, N % 16, K not a multiple of 512); the engine then uses
-    torch.matmul.  Engine-side op: the reference runs these projections
-    through torch.matmul (engine/models/llama.py:94-174).
+    not take (M > 16, N % 16, K outside {2048, 3072, 4096}, K = 8192 needs
+    M <= 8 and no SwiGLU); the engine then uses torch.matmul.  Engine-side op:
+    the reference runs these projections through torch.matmul
+    (engine/models/llama.py:94-174).
     """
-    dev = _on_gpu("decode_gemm", x, weight)
-    code = _dtype_code(x, "decode_gemm x")
-    _check(weight.dtype == x.dtype, "decode_gemm: weight dtype must match x")
-    _check(x.dim() == 2 and weight.dim() == 2 and x.size(1) == weight.size(1),
-           f"decode_gemm: x [M, K] and weight [N, K] expected (got {tuple(x.shape)}, "
-           f"{tuple(weight.shape)})")
-    _check(epilogue in _EPILOGUES, f"decode_gemm: unknown epilogue {epilogue!r}")
-    _check(x.stride(1) == 1 and weight.is_contiguous(),
-           "decode_gemm: x last dim and weight must be contiguous")
-    m, k = x.shape
-    n = weight.size(0) // 2 if epilogue == "swiglu" else weight.size(0)
-    _check(epilogue != "swiglu" or weight.size(0) % 2 == 0,
-           "decode_gemm: swiglu weight needs an even number of rows")
-    if out is None:
-        _check(epilogue != "add", "decode_gemm: epilogue 'add' needs out")
-        out = torch.empty(m, n, dtype=x.dtype, device=x.device)
-    _check(out.dtype == x.dtype and out.dim() == 2 and tuple(out.shape) == (m, n) and
-           out.stride(1) == 1 and out.device == x.device,
-           f"decode_gemm: out must be [{m}, {n}] with a contiguous last dim")
+    dev, code, m, n, k, out = _projection("decode_gemm", x, weight, out, epilogue)
     with _on_device(dev):
         _lib.call("mce_decode_gemm", code, x.data_ptr(), weight.data_ptr(), out.data_ptr(),
                   m, n, k, x.stride(0), out.stride(0), _EPILOGUES[epilogue], _stream(dev))
+    return out
+
+
+def rmsnorm_decode_gemm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                        weight: torch.Tensor, out: torch.Tensor = None,
+                        epilogue: str = "store") -> torch.Tensor:
+    """decode_gemm(rmsnorm(x, norm_weight, eps), weight, out, epilogue) in one
+    launch; the normalised rows are bit-identical to rmsnorm()'s and are not
+    written out.  K in {2048, 3072, 4096}.  Replaces the RMSNorm + projection
+    pairs of engine/models/llama.py:104-110 and :143-147."""
+    dev, code, m, n, k, out = _projection("rmsnorm_decode_gemm", x, weight, out, epilogue)
+    _check(norm_weight.device == x.device and norm_weight.dtype == x.dtype and
+           norm_weight.dim() == 1 and norm_weight.numel() == k and norm_weight.is_contiguous(),
+           f"rmsnorm_decode_gemm: norm_weight must be a contiguous [{k}] tensor like x")
+    with _on_device(dev):
+        _lib.call("mce_rmsnorm_decode_gemm", code, x.data_ptr(), norm_weight.data_ptr(),
+                  float(eps), weight.data_ptr(), out.data_ptr(), m, n, k, x.stride(0),
+                  out.stride(0), _EPILOGUES[epilogue], _stream(dev))
     return out
 
 

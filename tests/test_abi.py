@@ -16,6 +16,7 @@ HEADER_ENTRY_POINTS = {
     "mce_paged_kv_store", "mce_paged_attention_decode_workspace_size",
     "mce_paged_attention_decode", "mce_rope_inplace", "mce_prefill_attention",
     "mce_rope_kv_store", "mce_decode_gemm", "mce_paged_attention_decode_rope",
+    "mce_rmsnorm_decode_gemm",
 }
 
 
@@ -129,16 +130,33 @@ def test_rope_kv_store_validation(lib):
 
 def test_decode_gemm_validation(lib):
     f = lib.mce_decode_gemm
-    assert f(0, None, None, None, 8, 64, 512, 512, 64, 0, None) == _lib.MCE_ERR_INVALID
+    assert f(0, None, None, None, 8, 64, 2048, 2048, 64, 0, None) == _lib.MCE_ERR_INVALID
     assert "null" in _err(lib)
-    assert f(0, None, None, None, 8, 64, 512, 512, 64, 7, None) == _lib.MCE_ERR_INVALID
-    assert f(0, None, None, None, 17, 64, 512, 512, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
-    assert f(0, None, None, None, 8, 60, 512, 512, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
-    assert f(0, None, None, None, 8, 64, 500, 512, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
-    assert f(0, None, None, None, 8, 64, 8704, 8704, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(0, None, None, None, 8, 64, 2048, 2048, 64, 7, None) == _lib.MCE_ERR_INVALID
+    assert f(0, None, None, None, 17, 64, 2048, 2048, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(0, None, None, None, 8, 60, 2048, 2048, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(0, None, None, None, 8, 64, 512, 512, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(0, None, None, None, 8, 64, 2560, 2560, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
     assert f(0, None, None, None, 8, 64, 8192, 8192, 64, 2, None) == _lib.MCE_ERR_UNSUPPORTED
-    assert f(1, None, None, None, 8, 64, 512, 512, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
-    assert f(0, None, None, None, 0, 64, 512, 512, 64, 0, None) == _lib.MCE_OK
+    assert f(0, None, None, None, 9, 64, 8192, 8192, 64, 1, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(1, None, None, None, 8, 64, 2048, 2048, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
+    assert f(0, None, None, None, 0, 64, 2048, 2048, 64, 0, None) == _lib.MCE_OK
+
+
+def test_rmsnorm_decode_gemm_validation(lib):
+    f = lib.mce_rmsnorm_decode_gemm
+    one = ctypes.c_void_p(16)  # non-null, never dereferenced: validation fails first
+    assert f(0, None, None, 1e-5, None, None, 8, 64, 3072, 3072, 64, 0, None) == \
+        _lib.MCE_ERR_INVALID
+    assert "norm weight" in _err(lib)
+    assert f(0, None, one, -1.0, None, None, 8, 64, 3072, 3072, 64, 0, None) == \
+        _lib.MCE_ERR_INVALID
+    # k = 8192 is only taken without the fused RMSNorm
+    assert f(0, None, one, 1e-5, None, None, 8, 64, 8192, 8192, 64, 1, None) == \
+        _lib.MCE_ERR_UNSUPPORTED
+    assert f(0, None, one, 1e-5, None, None, 8, 64, 3072, 3072, 64, 2, None) == \
+        _lib.MCE_ERR_INVALID
+    assert "null" in _err(lib)
 
 
 def test_python_ops_reject_cpu_tensors():

@@ -41,9 +41,16 @@ def close(gpu, ref, rel=1e-2, abs_=5e-2):
     assert err.item() <= rel and mx <= abs_, (err.item(), mx)
 
 
-def test_prefill_then_eager_decode_match_oracle(dev):
+@pytest.mark.parametrize("projections", ["decode_gemm", "library"])
+def test_prefill_then_eager_decode_match_oracle(dev, projections, monkeypatch):
+    """Both decode-step paths: the decode-sized GEMM kernels with RMSNorm /
+    SwiGLU / residual fused (taken at this batch), and torch.matmul with the
+    separate ops (taken for larger batches, forced here)."""
     b, s = 2, 37
     model, cache, ref = build(dev, b, s, 4, tied=False)
+    assert model._decode_gemms_take(b)
+    if projections == "library":
+        monkeypatch.setattr(model, "_decode_gemms_take", lambda n: False)
     ids = torch.randint(0, CFG["vocab_size"], (b, s), generator=torch.Generator().manual_seed(1))
     logits = prefill_step(model, ids.to(dev), [0, 1], torch.full((b,), s, dtype=torch.int32))
     close(logits, ref.prefill(ids, [0, 1]))

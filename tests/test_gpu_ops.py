@@ -310,7 +310,7 @@ def test_cfg3_rope_kvstore_prefill_pipeline(dev):
 @pytest.mark.parametrize("m", [1, 5, 8, 16])
 @pytest.mark.parametrize("n,k,epi", [(5120, 3072, "store"), (3072, 3072, "add"),
                                      (8192, 3072, "swiglu"), (3072, 8192, "add"),
-                                     (1024, 512, "store")])
+                                     (1024, 2048, "store"), (512, 4096, "swiglu")])
 def test_decode_gemm_matches_fp32(dev, m, n, k, epi):
     """x . W^T for the decode step's projection shapes with the fused
     epilogues, against fp32 torch on the same fp16 inputs: plain store,
@@ -318,6 +318,8 @@ def test_decode_gemm_matches_fp32(dev, m, n, k, epi):
     [gate; up] weight (gate_up + SwiGLU).  x rows are strided (a view into a
     wider buffer) as the engine passes them."""
     from mycustomcudaengine_amd.ops import decode_gemm
+    if k == 8192 and m > 8:
+        pytest.skip("k = 8192 is taken for m <= 8 only (128 KB of staged x)")
     g = gen(80 + m + n // 512)
     rows = 2 * n if epi == "swiglu" else n
     xbuf = torch.randn(m, k + 64, generator=g).half()
@@ -340,6 +342,56 @@ def test_decode_gemm_matches_fp32(dev, m, n, k, epi):
         out = decode_gemm(xd, w.to(dev), epilogue=epi)
     ok, err = rel_close(out.cpu(), ref, 4e-3, 2e-3)
     assert ok, err
+
+
+@pytest.mark.parametrize("m", [1, 3, 8, 12, 16])
+@pytest.mark.parametrize("n,k,epi", [(5120, 3072, "store"), (8192, 3072, "swiglu"),
+                                     (1024, 2048, "add"), (512, 4096, "swiglu")])
+def test_rmsnorm_decode_gemm_equals_rmsnorm_then_gemm(dev, m, n, k, epi):
+    """The fused RMSNorm + projection gives exactly the bits of rmsnorm()
+    followed by decode_gemm() (same normalised rows, same GEMM), and matches
+    an fp32 reference of RMSNorm + projection (+ SwiGLU / residual add)."""
+    import my_cuda_engine_cpp as ops
+    from mycustomcudaengine_amd.ops import decode_gemm, rmsnorm_decode_gemm
+    g = gen(120 + m + n // 512)
+    rows = 2 * n if epi == "swiglu" else n
+    xbuf = (torch.randn(m, k + 64, generator=g) * 2).half()
+    nw = (1 + 0.1 * torch.randn(k, generator=g)).half()
+    w = (torch.randn(rows, k, generator=g) * 0.02).half()
+    res = torch.randn(m, n, generator=g).half()
+    xd, nwd, wd = xbuf.to(dev)[:, 32:32 + k], nw.to(dev), w.to(dev)
+    eps = 1e-5
+    if epi == "add":
+        fused, split = res.to(dev), res.to(dev)
+        rmsnorm_decode_gemm(xd, nwd, eps, wd, out=fused, epilogue="add")
+        decode_gemm(ops.rmsnorm(xd, nwd, eps), wd, out=split, epilogue="add")
+    else:
+        fused = rmsnorm_decode_gemm(xd, nwd, eps, wd, epilogue=epi)
+        split = decode_gemm(ops.rmsnorm(xd, nwd, eps), wd, epilogue=epi)
+    assert torch.equal(fused.view(torch.int16), split.view(torch.int16))
+    x = xbuf[:, 32:32 + k].float()
+    xn = x / torch.sqrt((x * x).mean(dim=1, keepdim=True) + eps) * nw.float()
+    acc = xn @ w.float().T
+    if epi == "swiglu":
+        ref = acc[:, :n] * torch.sigmoid(acc[:, :n]) * acc[:, n:]
+    elif epi == "add":
+        ref = res.float() + acc
+    else:
+        ref = acc
+    ok, err = rel_close(fused.cpu(), ref, 4e-3, 2e-3)
+    assert ok, err
+
+
+def test_rmsnorm_engine_width_matches_fp32(dev):
+    """mce_rmsnorm's rows against an fp32 reference at the engine's width."""
+    import my_cuda_engine_cpp as ops
+    g = gen(140)
+    x = (torch.randn(8, 3072, generator=g) * 3).half()
+    w = (1 + 0.1 * torch.randn(3072, generator=g)).half()
+    y = ops.rmsnorm(x.to(dev), w.to(dev), 1e-5).cpu().float()
+    xf = x.float()
+    ref = xf / torch.sqrt((xf * xf).mean(dim=1, keepdim=True) + 1e-5) * w.float()
+    assert (y - ref).abs().max().item() <= 2e-2
 
 
 def test_decode_gemm_rejects_unsupported_shapes(dev):
