@@ -18,10 +18,11 @@
 //     of one group) both hit 16 different 16-byte bank groups;
 //   * W fragments (A operand: lane l holds row l % 16, k 8 (l / 16) .. +7) go
 //     from HBM straight into registers: the x loads are issued first (loads
-//     return in order, so staging x waits for x only), then the first half of
-//     the W fragments, then x is staged and the second half issued.  Register
-//     use stays low enough for every workgroup of a launch to be resident, so
-//     the whole weight is in flight at once;
+//     return in order, so staging x waits for x only), then the W fragments
+//     -- all of them, or half when registers are short (SwiGLU's two tiles),
+//     the rest issued once x is staged.  Register use stays low enough for
+//     every workgroup of a launch to be resident, so the whole weight is in
+//     flight at once;
 //   * one v_mfma_f32_16x16x32_f16 per chunk and tile (tokens >= M are zeros);
 //     the 8 K-slice partials (lane l: rows 4 (l / 16) .. +3, token l % 16)
 //     are summed in LDS and wave 0 applies the epilogue:
@@ -66,7 +67,11 @@ void decode_gemm_kernel(DecodeGemmArgs a) {
   constexpr int K = C * 256;
   constexpr int VPT = K / 512;      // 16-byte groups of one token row per lane
   constexpr int NTOK = MP / 8;      // token rows staged per wave
-  constexpr int C1 = (C + 1) / 2;   // W chunks fetched before x is staged
+  // W chunks fetched before x is staged: all of them when the registers of
+  // the W fragments, the x rows and the norm weights fit the occupancy
+  // target together, else half (the rest once x is in LDS)
+  constexpr int REGS = 4 * (TT * C + NTOK * VPT + (NORM ? VPT : 0)) + 24;
+  constexpr int C1 = REGS <= 512 / WPE ? C : (C + 1) / 2;
   __shared__ __attribute__((aligned(16))) uint16_t xs[K / 8 * MP * 8];
   static_assert(K / 8 * MP * 8 * 2 >= DG_WAVES * TT * 4 * 64 * 4, "reduction fits");
 
@@ -104,6 +109,9 @@ void decode_gemm_kernel(DecodeGemmArgs a) {
   for (int c = 0; c < C1; ++c)
 #pragma unroll
     for (int t = 0; t < TT; ++t) wf[t][c] = *reinterpret_cast<const u32x4 *>(wp[t] + 32 * c);
+  // keep these loads ahead of the staging below (the scheduler would
+  // otherwise sink most of them past it to save registers)
+  __builtin_amdgcn_sched_barrier(0);
 
   // 3. stage x (normalised) into LDS; slots of tokens >= M hold zeros
 #pragma unroll
