@@ -228,8 +228,9 @@ MCE_API int mce_decode_gemm(int dtype, const void *x, const void *w, void *out, 
  * output; same epilogues, layouts and shape rules as mce_decode_gemm, k in
  * {2048, 3072, 4096}.  The normalised rows are not written out.  Replaces the
  * RMSNorm + projection pairs of the reference decode step
- * (engine/models/llama.py:104-110 input_layernorm + q/k/v, :143-147
- * post_attention_layernorm + gate/up, with csrc/kernels/rmsnorm.cu:35-130).
+ * (engine/models/llama.py:82-108 input_layernorm + q/k/v, :147-159
+ * post_attention_layernorm + gate/up, :169-174 final norm + lm_head; with
+ * csrc/kernels/rmsnorm.cu:35-130).
  */
 MCE_API int mce_rmsnorm_decode_gemm(int dtype, const void *x, const void *norm_weight, float eps,
                                     const void *w, void *out, int m, int n, int k,

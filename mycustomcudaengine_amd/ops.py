@@ -410,7 +410,7 @@ def rmsnorm_decode_gemm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     """decode_gemm(rmsnorm(x, norm_weight, eps), weight, out, epilogue) in one
     launch; the normalised rows are bit-identical to rmsnorm()'s and are not
     written out.  K in {2048, 3072, 4096}.  Replaces the RMSNorm + projection
-    pairs of engine/models/llama.py:104-110 and :143-147."""
+    pairs of engine/models/llama.py:82-108, :147-159 and :169-174."""
     dev, code, m, n, k, out = _projection("rmsnorm_decode_gemm", x, weight, out, epilogue)
     _check(norm_weight.device == x.device and norm_weight.dtype == x.dtype and
            norm_weight.dim() == 1 and norm_weight.numel() == k and norm_weight.is_contiguous(),
