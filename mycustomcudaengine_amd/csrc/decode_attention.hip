@@ -101,11 +101,12 @@ __device__ inline int clamp_ctx(int c, int cap) { return c < 0 ? 0 : (c > cap ? 
 // Exclusive prefix sum of per-sequence split weights (tiles + SEG_TILES for a
 // non-empty sequence) into pre[0..B]; returns NT.  Sequence b's real tiles
 // are [pre[b] + SEG_TILES, pre[b+1]).
+template <int NW>
 __device__ int build_tile_prefix(const DecodeArgs &a, int *pre, int *wave_tot) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int cap = a.maxb << a.bs_log2;
   int carry = 0;
-  for (int base = 0; base < a.B; base += NT_THREADS) {
+  for (int base = 0; base < a.B; base += NW * 64) {
     const int b = base + tid;
     int v = b < a.B ? (clamp_ctx(a.ctx_lens[b], cap) + TILE - 1) / TILE : 0;
     if (v > 0) v += SEG_TILES;
@@ -121,7 +122,7 @@ __device__ int build_tile_prefix(const DecodeArgs &a, int *pre, int *wave_tot) {
     for (int ww = 0; ww < w; ++ww) before += wave_tot[ww];
     if (b < a.B) pre[b] = before + incl - v;
     int total = 0;
-    for (int ww = 0; ww < DEC_NW; ++ww) total += wave_tot[ww];
+    for (int ww = 0; ww < NW; ++ww) total += wave_tot[ww];
     carry += total;
     lds_barrier();
   }
@@ -146,28 +147,39 @@ __device__ inline u32x4 ld_nt(const uint16_t *p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
 }
 
+// cos / sin of the lane's four rotation pairs (dims 8 (lr & 7) .. +7 of the
+// first half), fetched apart from the rotation so the loads can be issued early
+struct RopeCS {
+  floatx4 c0, c1, s0, s1;
+};
+
+__device__ inline RopeCS rope_fetch(const DecodeArgs &a, int pos, int lr) {
+  const int i0 = 8 * (lr & 7);  // rotation index of the lane's first dim
+  const float *cp = a.rope_cos + (int64_t)pos * (HD / 2) + i0;
+  const float *sp = a.rope_sin + (int64_t)pos * (HD / 2) + i0;
+  RopeCS r;
+  r.c0 = *reinterpret_cast<const floatx4 *>(cp);
+  r.c1 = *reinterpret_cast<const floatx4 *>(cp + 4);
+  r.s0 = *reinterpret_cast<const floatx4 *>(sp);
+  r.s1 = *reinterpret_cast<const floatx4 *>(sp + 4);
+  return r;
+}
+
 // RoPE of one 128-dim head row spread over a 16-lane group: lane lr holds
 // dims 8 lr .. 8 lr + 7; the rotation pairs dim i < 64 with i + 64, i.e. lane
 // lr with lane lr ^ 8 (all 64 lanes take part in the exchange).  Returns the
 // lane's rotated 8 values, rounded as rope_inplace rounds them.
 template <class T>
-__device__ inline u32x4 rope_rows(const u32x4 x, const DecodeArgs &a, int pos, int lr) {
+__device__ inline u32x4 rope_apply(const u32x4 x, const RopeCS &r, int lr) {
   u32x4 pt;
 #pragma unroll
   for (int k = 0; k < 4; ++k) pt[k] = (uint32_t)__shfl_xor((int)x[k], 8, 64);
   const bool lo_half = lr < 8;
-  const int i0 = 8 * (lr & 7);  // rotation index of the lane's first dim
-  const float *cp = a.rope_cos + (int64_t)pos * (HD / 2) + i0;
-  const float *sp = a.rope_sin + (int64_t)pos * (HD / 2) + i0;
-  const floatx4 c0 = *reinterpret_cast<const floatx4 *>(cp);
-  const floatx4 c1 = *reinterpret_cast<const floatx4 *>(cp + 4);
-  const floatx4 s0 = *reinterpret_cast<const floatx4 *>(sp);
-  const floatx4 s1 = *reinterpret_cast<const floatx4 *>(sp + 4);
   u32x4 o;
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const float cl = k < 2 ? c0[2 * k] : c1[2 * k - 4], ch = k < 2 ? c0[2 * k + 1] : c1[2 * k - 3];
-    const float sl = k < 2 ? s0[2 * k] : s1[2 * k - 4], sh = k < 2 ? s0[2 * k + 1] : s1[2 * k - 3];
+    const float cl = k < 2 ? r.c0[2 * k] : r.c1[2 * k - 4], ch = k < 2 ? r.c0[2 * k + 1] : r.c1[2 * k - 3];
+    const float sl = k < 2 ? r.s0[2 * k] : r.s1[2 * k - 4], sh = k < 2 ? r.s0[2 * k + 1] : r.s1[2 * k - 3];
     // (x0, x1) = (dim i, dim i + 64) of this element pair
     const float a0 = T::lo(lo_half ? x[k] : pt[k]), a1 = T::lo(lo_half ? pt[k] : x[k]);
     const float b0 = T::hi(lo_half ? x[k] : pt[k]), b1 = T::hi(lo_half ? pt[k] : x[k]);
@@ -179,11 +191,14 @@ __device__ inline u32x4 rope_rows(const u32x4 x, const DecodeArgs &a, int pos, i
   return o;
 }
 
-// Two waves per SIMD: one 8-wave workgroup per CU.  (GQA groups of 7 or 8
-// query heads per kv head spill a few registers at this occupancy.)
-template <class T, int G>
-__global__ __launch_bounds__(NT_THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+// Two waves per SIMD: one NW = 8-wave workgroup per CU.  (GQA groups of 7 or
+// 8 query heads per kv head spill a few registers at this occupancy.)
+// FUSED: RoPE + KV append of the new token (per-sequence mode only; a.knew
+// set), a separate instantiation so the plain kernels carry none of its state.
+template <class T, int G, int NW, bool FUSED>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW / 4)))
 void paged_decode_kernel(DecodeArgs a) {
+  constexpr int NTH = NW * 64;
   // per-sequence mode: blockIdx.x = slice * Hkv + kv head (the gsplit
   // workgroups of one kv head share an XCD when Hkv is a multiple of 8)
   const int gsub = a.per_seq ? (int)blockIdx.x / a.Hkv : 0;  // query-head slice
@@ -201,13 +216,21 @@ void paged_decode_kernel(DecodeArgs a) {
   const int head0 = g * gq + gsub * G;           // this wave's G query heads
 
   __shared__ int pre[MAX_BATCH + 1];
-  __shared__ int wave_tot[DEC_NW];
+  __shared__ int wave_tot[NW];
   __shared__ int blk_lds[MAX_IDS];
   const int nb_hi = (int)(a.num_blocks - 1 < 0x7fffffff ? a.num_blocks - 1 : 0x7fffffff);
-  __shared__ float red_acc[DEC_NW][G][HD];
-  __shared__ float red_m[DEC_NW][G], red_l[DEC_NW][G];
+  __shared__ float red_acc[NW][G][HD];
+  __shared__ float red_m[NW][G], red_l[NW][G];
 
   int NT, je, seg0;  // seg0: virtual tiles at the start of each sequence
+  int ctx_j = 0;     // per-sequence mode: the context length, kept for the tile loop
+  // fused RoPE + KV append (per-sequence mode): the new token's state
+  int pos_j = 0;
+  int64_t slot_j = -1;  // -1: no store, nothing to substitute
+  bool rope_ok = false;
+  RopeCS cs_new{};
+  u32x4 kx_new{}, vx_new{}, q_pre[G];
+  __shared__ u32x4 knv_lds[32];  // rotated k (lanes 0-15) and v (16-31) of the new token
   if (a.per_seq) {
     seg0 = 0;
     // one workgroup per (head group, sequence j): a one-sequence tile space
@@ -215,47 +238,55 @@ void paged_decode_kernel(DecodeArgs a) {
     // and the rows are written directly (no merge pass).  The sequence's
     // block ids (at most PER_SEQ_MAX_TOKENS / MIN_BS of them) are fetched
     // together with its context length.
+    // (maxb <= PER_SEQ_MAX_TOKENS / MIN_BS <= NTH: one block id per thread)
     const int32_t *btj = a.btab + (int64_t)j * a.maxb;
-    for (int i = tid; i < a.maxb; i += NT_THREADS) {
-      const int v = btj[i];
-      blk_lds[i] = v < 0 ? 0 : (v > nb_hi ? nb_hi : v);
+    const int bt_v = tid < a.maxb ? btj[tid] : 0;
+    ctx_j = clamp_ctx(a.ctx_lens[j], cap);
+    if constexpr (FUSED) {
+      // Fused RoPE + KV append: the new token's position, slot and k / v rows
+      // and this wave's query rows are fetched with the block ids, the
+      // cos / sin rows as soon as the position is known.  The rotations, the
+      // slot stores and an LDS copy of the new k / v row follow once the first
+      // tile's loads are issued (tile loop below).  The stores are not waited
+      // for: every K / V row the workgroup loads from the new slot is taken
+      // from the LDS copy, which is what reading after the store returns.
+      pos_j = a.positions[j];
+      const int64_t sl = a.slots[j];
+      slot_j = sl >= 0 && sl < a.num_slots ? sl : -1;
+      rope_ok = pos_j >= 0 && pos_j < a.table_rows;
+      const int64_t row = (int64_t)j * a.new_stride_b + (int64_t)g * HD + lr * 8;
+      kx_new = *reinterpret_cast<const u32x4 *>(a.knew + row);
+      vx_new = *reinterpret_cast<const u32x4 *>(a.vnew + row);
+#pragma unroll
+      for (int h = 0; h < G; ++h)
+        q_pre[h] = *reinterpret_cast<const u32x4 *>(a.query + (int64_t)j * a.q_stride_b +
+                                                    (int64_t)(head0 + h) * HD + lr * 8);
+      if (rope_ok) cs_new = rope_fetch(a, pos_j, lr);
     }
+    if (tid < a.maxb) blk_lds[tid] = bt_v < 0 ? 0 : (bt_v > nb_hi ? nb_hi : bt_v);
     if (tid == 0) {
       pre[j] = 0;
-      pre[j + 1] = (clamp_ctx(a.ctx_lens[j], cap) + TILE - 1) / TILE;
+      pre[j + 1] = (ctx_j + TILE - 1) / TILE;
     }
-    if (a.knew) {
-      // The new token's k (rotated) and v into its page slot, by wave 0
-      // (lane lr: dims 8 lr .. 8 lr + 7, pair partner in lane lr ^ 8).  Every
-      // workgroup of this kv head writes the same bytes and only then reads
-      // the sequence, so each sees its own write.
-      if (w == 0) {
-        const int64_t slot = a.slots[j];
-        const int pos = a.positions[j];
-        const int64_t row = (int64_t)j * a.new_stride_b + (int64_t)g * HD + lr * 8;
-        u32x4 kx = *reinterpret_cast<const u32x4 *>(a.knew + row);
-        const u32x4 vx = *reinterpret_cast<const u32x4 *>(a.vnew + row);
-        if (pos >= 0 && pos < a.table_rows) kx = rope_rows<T>(kx, a, pos, lr);
-        if (lg == 0 && slot >= 0 && slot < a.num_slots) {
-          const int64_t dst = (slot * a.Hkv + g) * HD + lr * 8;
-          *reinterpret_cast<u32x4 *>(const_cast<uint16_t *>(a.kcache) + dst) = kx;
-          *reinterpret_cast<u32x4 *>(const_cast<uint16_t *>(a.vcache) + dst) = vx;
-        }
-      }
-      __syncthreads();  // the slot's stores are complete before any K/V load
-    } else {
-      lds_barrier();
-    }
+    lds_barrier();
     NT = pre[j + 1];
     je = 1;
     if (NT == 0) {
-      for (int i = tid; i < G * HD; i += NT_THREADS)
+      for (int i = tid; i < G * HD; i += NTH)
         a.out[((int64_t)j * a.Hq + head0) * HD + i] = 0;
+      if (FUSED && w == 0) {  // an empty sequence still gets its new k / v
+        const u32x4 kx = rope_ok ? rope_apply<T>(kx_new, cs_new, lr) : kx_new;
+        if (lg == 0 && slot_j >= 0) {
+          const int64_t dst = (slot_j * a.Hkv + g) * HD + lr * 8;
+          *reinterpret_cast<u32x4 *>(const_cast<uint16_t *>(a.kcache) + dst) = kx;
+          *reinterpret_cast<u32x4 *>(const_cast<uint16_t *>(a.vcache) + dst) = vx_new;
+        }
+      }
       return;
     }
   } else {
     seg0 = SEG_TILES;
-    NT = build_tile_prefix(a, pre, wave_tot);
+    NT = build_tile_prefix<NW>(a, pre, wave_tot);
     je = partition_count(NT, a.J);
   }
   if (!a.per_seq && j == 0) {
@@ -264,10 +295,10 @@ void paged_decode_kernel(DecodeArgs a) {
     const int h_lo = hgrp * hpg * G, h_hi = min(a.Hkv, (hgrp + 1) * hpg) * G;
     for (int b = 0; b < a.B; ++b)
       if (pre[b + 1] == pre[b])
-        for (int i = tid; i < (h_hi - h_lo) * HD; i += NT_THREADS)
+        for (int i = tid; i < (h_hi - h_lo) * HD; i += NTH)
           a.out[((int64_t)b * a.Hq + h_lo) * HD + i] = 0;
     if (hgrp == 0)
-      for (int b = tid; b < a.B; b += NT_THREADS)
+      for (int b = tid; b < a.B; b += NTH)
         a.ws_nparts[b] = pre[b + 1] == pre[b]
                              ? 0
                              : owner_of(pre[b + 1] - 1, NT, je) -
@@ -296,7 +327,7 @@ void paged_decode_kernel(DecodeArgs a) {
   for (; b < a.B && pre[b] < t_hi; ++b) {
     const int r0 = pre[b] + seg0;  // first real tile of b in the split space
     if (pre[b + 1] == pre[b] || max(t_lo, r0) >= min(t_hi, pre[b + 1])) continue;
-    const int ctx = clamp_ctx(a.ctx_lens[b], cap);
+    const int ctx = a.per_seq ? ctx_j : clamp_ctx(a.ctx_lens[b], cap);
     const int seg_lo = max(t_lo, r0) - r0;             // tile index in b
     const int seg_hi = min(t_hi, pre[b + 1]) - r0;
     const int tok_lo = seg_lo * TILE;
@@ -309,16 +340,10 @@ void paged_decode_kernel(DecodeArgs a) {
     u32x4 qv[G];
 #pragma unroll
     for (int h = 0; h < G; ++h)
-      qv[h] = active ? *reinterpret_cast<const u32x4 *>(
-                           a.query + (int64_t)b * a.q_stride_b + (int64_t)(head0 + h) * HD + lr * 8)
-                     : u32x4{0, 0, 0, 0};
-    if (a.knew) {  // fused RoPE of the query (same rounding as rope_inplace)
-      const int pos = a.positions[b];
-      if (pos >= 0 && pos < a.table_rows) {
-#pragma unroll
-        for (int h = 0; h < G; ++h) qv[h] = rope_rows<T>(qv[h], a, pos, lr);
-      }
-    }
+      qv[h] = FUSED ? q_pre[h]  // fetched in the prologue, rotated in the tile loop
+                     : active ? *reinterpret_cast<const u32x4 *>(
+                                    a.query + (int64_t)b * a.q_stride_b + (int64_t)(head0 + h) * HD + lr * 8)
+                              : u32x4{0, 0, 0, 0};
 
     // m_run: running max of the raw scores (uniform over the wave);
     // l_grp: softmax denominator of this lane group's tokens;
@@ -345,7 +370,7 @@ void paged_decode_kernel(DecodeArgs a) {
       if (!a.per_seq) {
         const int nblk = ((t_end - 1) >> bs_log2) - first_blk + 1;
         lds_barrier();  // previous users of blk_lds are done
-        for (int i = tid; i < nblk; i += NT_THREADS) {
+        for (int i = tid; i < nblk; i += NTH) {
           const int v = bt[first_blk + i];
           blk_lds[i] = v < 0 ? 0 : (v > nb_hi ? nb_hi : v);
         }
@@ -367,7 +392,7 @@ void paged_decode_kernel(DecodeArgs a) {
         for (int s8 = 0; s8 < 8; ++s8) vv[s8] = ld_nt(vbase + off + s8 * slot_stride);
       };
       // ---- compute of one tile ----
-      auto compute_tile = [&](int t0, const u32x4 (&kk)[8], u32x4 (&vv)[8]) {
+      auto tile_body = [&](int t0, u32x4 (&kk)[8], u32x4 (&vv)[8]) {
         const int tv = t0 + 8 * lg;
         // scores: 4 v_dot2 over the lane's 8 dims, then a 16-lane DPP sum;
         // every lane of a group ends with the scores of the group's 8 tokens
@@ -441,12 +466,65 @@ void paged_decode_kernel(DecodeArgs a) {
           }
         }
       };
+      // Fused append: rows the tile read from the new token's slot are
+      // replaced by the LDS copy (load_tile read tokens tvc .. tvc + 7 of one
+      // block per lane group).  Wave-uniform branch: only the tile holding
+      // the slot is patched, in place, every row by a select (a conditional
+      // write of one row would become an indexed register write, which puts
+      // the tile in scratch memory).
+      auto compute_tile = [&](int t0, u32x4 (&kk)[8], u32x4 (&vv)[8]) {
+        int sub = -1;
+        if (FUSED && slot_j >= 0) {
+          const int tv = t0 + 8 * lg;
+          const int tvc = tv < t_end ? tv : t0;
+          const int64_t slot0 =
+              ((int64_t)blk_lds[(tvc >> bs_log2) - first_blk] << bs_log2) + (tvc & (bs - 1));
+          const int64_t dd = slot_j - slot0;
+          sub = dd >= 0 && dd < 8 ? (int)dd : -1;
+        }
+        if (__builtin_expect(__ballot(sub >= 0) != 0, 0)) {
+          const u32x4 kn = knv_lds[lr], vn = knv_lds[16 + lr];
+#pragma unroll
+          for (int s8 = 0; s8 < 8; ++s8) {
+            const bool hit = s8 == sub;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              kk[s8][e] = hit ? kn[e] : kk[s8][e];
+              vv[s8][e] = hit ? vn[e] : vv[s8][e];
+            }
+          }
+        }
+        tile_body(t0, kk, vv);
+      };
 
       // ---- software-pipelined tile loop: next tile's loads before compute ----
       const int ntile = (t_end - s_lo + TILE - 1) / TILE;
       u32x4 kA[8], kB[8], vA[8], vB[8];
       int k = rlane;
       if (k < ntile) load_tile(s_lo + TILE * k, kA, vA);
+      if constexpr (FUSED) {
+        // (per-sequence mode: every wave of the workgroup is active and
+        // reaches this barrier)  RoPE of the query rows and, by wave 0, of the
+        // new k (same rounding as rope_inplace); wave 0 writes the new k / v
+        // to the slot and to LDS.
+        if (rope_ok) {
+#pragma unroll
+          for (int h = 0; h < G; ++h) qv[h] = rope_apply<T>(qv[h], cs_new, lr);
+        }
+        if (w == 0) {
+          const u32x4 kx = rope_ok ? rope_apply<T>(kx_new, cs_new, lr) : kx_new;
+          if (lg == 0) {
+            knv_lds[lr] = kx;
+            knv_lds[16 + lr] = vx_new;
+            if (slot_j >= 0) {
+              const int64_t dst = (slot_j * a.Hkv + g) * HD + lr * 8;
+              *reinterpret_cast<u32x4 *>(const_cast<uint16_t *>(a.kcache) + dst) = kx;
+              *reinterpret_cast<u32x4 *>(const_cast<uint16_t *>(a.vcache) + dst) = vx_new;
+            }
+          }
+        }
+        lds_barrier();
+      }
       while (k < ntile) {
         int kn = k + wph;
         if (kn < ntile) load_tile(s_lo + TILE * kn, kB, vB);
@@ -527,7 +605,7 @@ void paged_decode_kernel(DecodeArgs a) {
     }
     lds_barrier();
     const int nheads = min(hpg, a.Hkv - hgrp * hpg);
-    for (int idx = tid; idx < nheads * G * HD; idx += NT_THREADS) {
+    for (int idx = tid; idx < nheads * G * HD; idx += NTH) {
       const int hh = idx / (G * HD), rem = idx - hh * G * HD;
       const int h = rem / HD, d = rem - h * HD;
       float M = -INFINITY;
@@ -779,7 +857,10 @@ int decode_impl(int dtype, const void *query, const void *key_cache, const void 
   const dim3 grid = per_seq ? dim3(num_kv_heads * gsplit, batch) : dim3(Lay.groups, Lay.J);
 #define MCE_DEC_CASE(TT, GG)                                                   \
   case GG:                                                                     \
-    paged_decode_kernel<TT, GG><<<grid, NT_THREADS, 0, st>>>(a);               \
+    if (a.knew)                                                                \
+      paged_decode_kernel<TT, GG, DEC_NW, true><<<grid, NT_THREADS, 0, st>>>(a); \
+    else                                                                       \
+      paged_decode_kernel<TT, GG, DEC_NW, false><<<grid, NT_THREADS, 0, st>>>(a); \
     break;
 #define MCE_DEC_LAUNCH(TT)                                                     \
   switch (Gw) {                                                                \
