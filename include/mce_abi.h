@@ -238,6 +238,35 @@ MCE_API int mce_rmsnorm_decode_gemm(int dtype, const void *x, const void *norm_w
                                     void *stream);
 
 /*
+ * Greedy token of each logits row: out[r] = index of the largest value of
+ * logits[r, 0:cols] (rows row_stride elements apart; NaN ranks above every
+ * number and the lower index wins among equals, as torch.argmax does).
+ * Replaces the host-side torch.argmax between replays of the reference's
+ * decode loop (benchmarks/benchmark_engine.py:255-265), so the next input
+ * ids stay on the device inside a captured graph.
+ */
+MCE_API int mce_argmax_rows(int dtype, const void *logits, int64_t rows, int64_t cols,
+                            int64_t row_stride, int64_t *out, void *stream);
+
+/*
+ * Prepares the next decode step on the device (one launch, capturable):
+ * when token_log is non-null, token_log[step * batch + b] = input_ids[b] for
+ * step = *step_counter (skipped past log_capacity rows) and *step_counter is
+ * incremented; then for every sequence b: positions[b] += 1,
+ * context_lens[b] += 1 and slot_mapping[b] = block_tables[b][p / block_size]
+ * * block_size + p % block_size for the new position p (-1 when p falls
+ * outside the max_blocks_per_seq-wide, zero-padded int32 table).  Replaces
+ * the host-side preparation of every replay in the reference
+ * (engine/runner.py:39-60 _prepare_inputs, :153-178 execute; slot rule of
+ * engine/cache.py:48-57).
+ */
+MCE_API int mce_decode_advance(const int32_t *block_tables, int32_t *positions,
+                               int32_t *context_lens, int32_t *slot_mapping,
+                               const int64_t *input_ids, int64_t *token_log,
+                               int32_t *step_counter, int batch, int max_blocks_per_seq,
+                               int block_size, int log_capacity, void *stream);
+
+/*
  * Causal prefill attention over contiguous Q/K/V, GQA:
  *   out[b, s, h, :] = sum_{t <= s} softmax_t(scale * q[b,s,h] . k[b,t,g]) v[b,t,g]
  * with g = h / (num_heads / num_kv_heads).  query/out contiguous

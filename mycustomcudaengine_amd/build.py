@@ -26,6 +26,7 @@ SOURCES = [
     "decode_attention.hip",
     "prefill_attention.hip",
     "decode_gemm.hip",
+    "decode_loop.hip",
 ]
 ARCH = "gfx950"
 

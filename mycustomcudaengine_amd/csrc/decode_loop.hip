@@ -1,0 +1,137 @@
+// Device-side preparation of the next decode step, so that a captured decode
+// graph can be replayed step after step with no host work in between:
+//   * mce_argmax_rows: greedy token of each logits row (the reference's
+//     benchmark loop takes torch.argmax of the logits between replays,
+//     benchmarks/benchmark_engine.py:255-265);
+//   * mce_decode_advance: appends those tokens to a token log, moves every
+//     sequence one position on and recomputes its slot from the device block
+//     table (the reference computes positions, context lengths and slots on
+//     the host and copies them in before every replay, engine/runner.py:
+//     39-60,153-176, with the slot rule of engine/cache.py:48-57).
+// Both are index work: bit-exact against the allocator's slot rule and
+// torch.argmax.
+#include "mce_common.h"
+
+namespace mce {
+
+constexpr int AM_THREADS = 512;
+
+// (value, index) order of argmax: larger value first, NaN above every number
+// (as torch.argmax ranks it), the lower index among equals.
+__device__ inline bool am_better(float a, int64_t ia, float b, int64_t ib) {
+  const bool na = a != a, nb = b != b;
+  if (na || nb) return na && (!nb || ia < ib);
+  return a > b || (a == b && ia < ib);
+}
+
+// one workgroup per row
+template <class T>
+__global__ __launch_bounds__(AM_THREADS) void argmax_rows_kernel(const uint16_t *__restrict__ x,
+                                                                 int64_t cols, int64_t stride,
+                                                                 int64_t *__restrict__ out) {
+  const int64_t row = blockIdx.x;
+  const uint16_t *xr = x + row * stride;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  float best = -INFINITY;
+  int64_t bi = cols;  // past the end: loses to every real element
+  for (int64_t c = tid; c < cols; c += AM_THREADS) {
+    const float v = T::lo(xr[c]);
+    if (am_better(v, c, best, bi)) {
+      best = v;
+      bi = c;
+    }
+  }
+  // the order is total, so the reduction order does not change the result
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const float ov = __shfl_xor(best, d, 64);
+    const int64_t oi = __shfl_xor(bi, d, 64);
+    if (am_better(ov, oi, best, bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  __shared__ float bv[AM_THREADS / 64];
+  __shared__ int64_t bix[AM_THREADS / 64];
+  if (lane == 0) {
+    bv[w] = best;
+    bix[w] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int k = 1; k < AM_THREADS / 64; ++k)
+      if (am_better(bv[k], bix[k], best, bi)) {
+        best = bv[k];
+        bi = bix[k];
+      }
+    out[row] = bi < cols ? bi : 0;
+  }
+}
+
+// one workgroup: the step counter is read by every thread before thread 0
+// moves it on
+__global__ __launch_bounds__(256) void decode_advance_kernel(
+    const int32_t *__restrict__ block_tables, int32_t *__restrict__ positions,
+    int32_t *__restrict__ context_lens, int32_t *__restrict__ slot_mapping,
+    const int64_t *__restrict__ input_ids, int64_t *__restrict__ token_log,
+    int32_t *__restrict__ step_counter, int batch, int max_blocks, int block_size,
+    int log_capacity) {
+  const int step = token_log ? step_counter[0] : 0;
+  __syncthreads();
+  if (token_log && threadIdx.x == 0) step_counter[0] = step + 1;
+  for (int b = threadIdx.x; b < batch; b += blockDim.x) {
+    if (token_log && step >= 0 && step < log_capacity)
+      token_log[(int64_t)step * batch + b] = input_ids[b];
+    const int pos = positions[b] + 1;
+    positions[b] = pos;
+    context_lens[b] = context_lens[b] + 1;
+    const int64_t blk = pos >= 0 ? pos / block_size : -1;
+    slot_mapping[b] = blk >= 0 && blk < max_blocks
+                          ? block_tables[(int64_t)b * max_blocks + blk] * block_size +
+                                pos % block_size
+                          : -1;
+  }
+}
+
+}  // namespace mce
+
+using namespace mce;
+
+extern "C" int mce_argmax_rows(int dtype, const void *logits, int64_t rows, int64_t cols,
+                               int64_t row_stride, int64_t *out, void *stream) {
+  clear_error();
+  MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16, "mce_argmax_rows: unknown dtype %d", dtype);
+  MCE_REQUIRE(rows >= 0 && cols >= 1 && row_stride >= cols, "mce_argmax_rows: bad shape");
+  if (rows == 0) return MCE_OK;
+  MCE_REQUIRE(logits && out, "mce_argmax_rows: null pointer");
+  MCE_REQUIRE(rows < ((int64_t)1 << 31), "mce_argmax_rows: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == MCE_F16)
+    argmax_rows_kernel<F16T><<<(unsigned)rows, AM_THREADS, 0, st>>>((const uint16_t *)logits, cols,
+                                                                    row_stride, out);
+  else
+    argmax_rows_kernel<BF16T><<<(unsigned)rows, AM_THREADS, 0, st>>>((const uint16_t *)logits,
+                                                                     cols, row_stride, out);
+  return check_launch("mce_argmax_rows");
+}
+
+extern "C" int mce_decode_advance(const int32_t *block_tables, int32_t *positions,
+                                  int32_t *context_lens, int32_t *slot_mapping,
+                                  const int64_t *input_ids, int64_t *token_log,
+                                  int32_t *step_counter, int batch, int max_blocks_per_seq,
+                                  int block_size, int log_capacity, void *stream) {
+  clear_error();
+  MCE_REQUIRE(batch >= 0 && max_blocks_per_seq >= 0 && block_size >= 1 && log_capacity >= 0,
+              "mce_decode_advance: bad shape");
+  if (batch == 0) return MCE_OK;
+  MCE_REQUIRE(block_tables && positions && context_lens && slot_mapping,
+              "mce_decode_advance: null pointer");
+  MCE_REQUIRE(!token_log || (input_ids && step_counter),
+              "mce_decode_advance: a token log needs input_ids and step_counter");
+  MCE_REQUIRE((int64_t)max_blocks_per_seq * block_size < ((int64_t)1 << 31),
+              "mce_decode_advance: block table too wide");
+  decode_advance_kernel<<<1, 256, 0, (hipStream_t)stream>>>(
+      block_tables, positions, context_lens, slot_mapping, input_ids, token_log, step_counter,
+      batch, max_blocks_per_seq, block_size, log_capacity);
+  return check_launch("mce_decode_advance");
+}

@@ -18,13 +18,22 @@ Differences from the reference:
   * no clone of the whole KV cache around warm-up/capture: a decode step
     writes only its own slot before any attention reads it, so warm-up
     writes are overwritten by the first real step at that slot (the
-    reference clones kv_cache twice, runner.py:108,128,147).
+    reference clones kv_cache twice, runner.py:108,128,147);
+  * capture_graph(..., device_steps=n) also records the greedy token
+    (ops.argmax_rows into the static input ids) and the next step's
+    preparation (ops.decode_advance: positions, context lengths and slots
+    from the device block table, the token appended to a log), so
+    run_device_loop(k) replays k steps back to back with no host work in
+    between (the reference prepares every step on the host, runner.py:39-60,
+    153-178, and takes the argmax between replays, benchmark_engine.py:265).
 """
 from __future__ import annotations
 
 from typing import List, Optional, Tuple
 
 import torch
+
+from ..ops import argmax_rows, decode_advance
 
 
 class CUDAGraphRunner:
@@ -35,6 +44,8 @@ class CUDAGraphRunner:
         self.cuda_graph: Optional[torch.cuda.CUDAGraph] = None
         self.is_captured = False
         self.max_blocks_per_seq = 0
+        self.device_steps = 0
+        self._ctx: List[int] = []
         self._alloc_static(max_batch_size, 1)
 
     def _alloc_static(self, batch: int, max_blocks: int) -> None:
@@ -70,7 +81,7 @@ class CUDAGraphRunner:
 
     def capture_graph(self, input_ids: torch.Tensor, positions: torch.Tensor,
                       seq_ids: List[int], context_lens, max_blocks: Optional[int] = None,
-                      warmup: int = 3) -> None:
+                      warmup: int = 3, device_steps: int = 0) -> None:
         cache = self.model.cache_manager
         b = input_ids.size(0)
         ctx = self._host_ints(context_lens)
@@ -87,11 +98,24 @@ class CUDAGraphRunner:
             for _ in range(warmup):
                 self._step(b)
         s.synchronize()
+        self.device_steps = int(device_steps)
+        if self.device_steps > 0:
+            self.token_log = torch.zeros((self.device_steps, b), dtype=torch.int64,
+                                         device=self.device)
+            self.step_counter = torch.zeros((1,), dtype=torch.int32, device=self.device)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.stream(s):
             with torch.cuda.graph(graph, stream=s):
                 out = self._step(b)
                 self.static_logits.copy_(out)
+                if self.device_steps > 0:
+                    # greedy token -> next input ids; next step's positions,
+                    # context lengths and slots, all on the device
+                    argmax_rows(self.static_logits[:b], out=self.static_input_ids[:b])
+                    decode_advance(self.static_block_tables[:b], self.static_positions[:b],
+                                   self.static_context_lens[:b], self.static_slot_mapping[:b],
+                                   cache.block_size, input_ids=self.static_input_ids[:b],
+                                   token_log=self.token_log, step_counter=self.step_counter)
         s.synchronize()
         torch.cuda.current_stream(self.device).wait_stream(s)
         self.cuda_graph = graph
@@ -101,6 +125,7 @@ class CUDAGraphRunner:
     def _fill(self, input_ids, positions, seq_ids, ctx: List[int]) -> None:
         b = len(seq_ids)
         cache = self.model.cache_manager
+        self._seq_ids, self._ctx = list(seq_ids), list(ctx)
         self.static_input_ids[:b].copy_(input_ids)
         self.static_positions[:b].copy_(positions)
         self.static_context_lens[:b].copy_(torch.tensor(ctx, dtype=torch.int32))
@@ -119,4 +144,26 @@ class CUDAGraphRunner:
             raise RuntimeError("context exceeds the block-table width captured in the graph")
         self._fill(input_ids, positions, seq_ids, ctx)
         self.cuda_graph.replay()
+        if self.device_steps > 0:  # the replay also prepared the next step
+            self._ctx = [c + 1 for c in ctx]
         return self.static_logits[:b]
+
+    def run_device_loop(self, steps: int) -> torch.Tensor:
+        """Replays the captured step `steps` times back to back, each replay
+        feeding its greedy token and its successor's slots to the next on the
+        device; starts from the state of the last capture_graph / execute.
+        Returns the [steps, B] int64 log of generated tokens (a view of the
+        runner's buffer).  Needs capture_graph(..., device_steps >= steps) and
+        every sequence's blocks allocated for the positions it reaches."""
+        assert self.is_captured, "CUDA Graph must be captured before execution!"
+        if steps > self.device_steps:
+            raise RuntimeError(f"graph captured for {self.device_steps} device steps, got {steps}")
+        cache = self.model.cache_manager
+        for s, c in zip(self._seq_ids, self._ctx):
+            if c + steps - 1 > len(cache.block_tables[s]) * cache.block_size:
+                raise RuntimeError(f"sequence {s} has no block for position {c + steps - 2}")
+        self.step_counter.zero_()
+        for _ in range(steps):
+            self.cuda_graph.replay()
+        self._ctx = [c + steps for c in self._ctx]
+        return self.token_log[:steps]

@@ -422,6 +422,68 @@ def rmsnorm_decode_gemm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     return out
 
 
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
+    """Greedy token of each row of logits [R, C] (fp16 / bf16, contiguous last
+    dim): int64 [R], torch.argmax's rule (the first of equal maxima, NaN above
+    every number).  `out` may be any contiguous int64 tensor of R elements
+    (e.g. the [R, 1] input ids of the next step).  Replaces the torch.argmax
+    between replays of benchmarks/benchmark_engine.py:255-265."""
+    dev = _on_gpu("argmax_rows", logits)
+    code = _dtype_code(logits, "argmax_rows logits")
+    _check(logits.dim() == 2 and logits.stride(1) == 1 and logits.size(1) >= 1,
+           "argmax_rows: logits must be [R, C] with a contiguous last dim")
+    r = logits.size(0)
+    if out is None:
+        out = torch.empty(r, dtype=torch.int64, device=logits.device)
+    _check(out.dtype == torch.int64 and out.numel() == r and out.is_contiguous() and
+           out.device == logits.device, f"argmax_rows: out must be {r} contiguous int64 values")
+    with _on_device(dev):
+        _lib.call("mce_argmax_rows", code, logits.data_ptr(), r, logits.size(1), logits.stride(0),
+                  out.data_ptr(), _stream(dev))
+    return out
+
+
+def decode_advance(block_tables: torch.Tensor, positions: torch.Tensor,
+                   context_lens: torch.Tensor, slot_mapping: torch.Tensor, block_size: int,
+                   input_ids: torch.Tensor = None, token_log: torch.Tensor = None,
+                   step_counter: torch.Tensor = None) -> None:
+    """Prepares the next decode step on the device, in place: positions and
+    context_lens move one on, slot_mapping gets the new positions' slots from
+    block_tables ([B, W] int32, zero-padded, blocks of block_size tokens; -1
+    past W).  With token_log
+    ([steps, B] int64) input_ids ([B] or [B, 1] int64) is first written to row
+    step_counter[0] (int32, incremented).  Replaces the host-side
+    preparation of every replay in engine/runner.py:39-60,153-178."""
+    dev = _on_gpu("decode_advance", block_tables, positions, context_lens, slot_mapping)
+    _check(block_size >= 1, "decode_advance: block_size must be >= 1")
+    _check(block_tables.dtype == torch.int32 and block_tables.dim() == 2 and
+           block_tables.is_contiguous(), "decode_advance: block_tables must be contiguous int32 [B, W]")
+    b, w = block_tables.shape
+    for name, t in (("positions", positions), ("context_lens", context_lens),
+                    ("slot_mapping", slot_mapping)):
+        _check(t.dtype == torch.int32 and t.numel() == b and t.is_contiguous() and t.device == dev,
+               f"decode_advance: {name} must be {b} contiguous int32 values")
+    log_ptr = ids_ptr = ctr_ptr = 0
+    cap = 0
+    if token_log is not None:
+        _check(input_ids is not None and step_counter is not None,
+               "decode_advance: token_log needs input_ids and step_counter")
+        _check(token_log.dtype == torch.int64 and token_log.dim() == 2 and token_log.size(1) == b
+               and token_log.is_contiguous() and token_log.device == dev,
+               f"decode_advance: token_log must be contiguous int64 [steps, {b}]")
+        _check(input_ids.dtype == torch.int64 and input_ids.numel() == b and
+               input_ids.is_contiguous() and input_ids.device == dev,
+               f"decode_advance: input_ids must be {b} contiguous int64 values")
+        _check(step_counter.dtype == torch.int32 and step_counter.numel() >= 1 and
+               step_counter.device == dev, "decode_advance: step_counter must be int32")
+        log_ptr, ids_ptr, ctr_ptr = token_log.data_ptr(), input_ids.data_ptr(), step_counter.data_ptr()
+        cap = token_log.size(0)
+    with _on_device(dev):
+        _lib.call("mce_decode_advance", block_tables.data_ptr(), positions.data_ptr(),
+                  context_lens.data_ptr(), slot_mapping.data_ptr(), ids_ptr, log_ptr, ctr_ptr, b, w,
+                  int(block_size), cap, _stream(dev))
+
+
 def prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                       scale: float) -> torch.Tensor:
     """Causal GQA attention on contiguous Q/K/V (reference: prefill_attention.cu:271-309).

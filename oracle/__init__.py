@@ -24,6 +24,9 @@ How each function is pinned (tests/test_oracle.py):
   kv_store_ref           scalar Python loop; slot < 0 skipped.
   BlockAllocatorRef      hand-enumerated FIFO sequences.
   slot_mapping_ref       brute force over the allocator's tables.
+  decode_advance_ref     the allocator's slot_of() on the positions it yields,
+                         -1 past the table width (hand-built cases).
+  argmax_rows_ref        numpy.argmax; torch.argmax on ties and NaN rows.
   llama_*_ref            composition of the above with fp32 GEMMs; checked
                          against a torch-only decomposition of one layer.
 """

@@ -58,3 +58,28 @@ def prefill_slots_ref(tables: dict, seq_ids, seq_len: int, block_size: int) -> n
         for p in range(seq_len):
             out[i, p] = tables[s][p // block_size] * block_size + p % block_size
     return out.reshape(-1)
+
+
+def decode_advance_ref(table: np.ndarray, positions, context_lens, block_size: int):
+    """One step of device-side decode preparation, restated from the slot rule
+    of engine/cache.py:48-57 and engine/runner.py:49-55 (reference): every
+    sequence moves one position on (context length too) and its new slot is
+    table[b, p // BS] * BS + p % BS on the zero-padded [B, W] int32 table, -1
+    when the new position p falls outside the W blocks.  Returns (positions,
+    context_lens, slots) as new int32 arrays."""
+    table = np.asarray(table, dtype=np.int64)
+    pos = np.asarray(positions, dtype=np.int64).reshape(-1) + 1
+    ctx = np.asarray(context_lens, dtype=np.int64).reshape(-1) + 1
+    slots = np.full(pos.shape, -1, dtype=np.int64)
+    for b in range(pos.size):
+        blk = pos[b] // block_size
+        if pos[b] >= 0 and blk < table.shape[1]:
+            slots[b] = table[b, blk] * block_size + pos[b] % block_size
+    return pos.astype(np.int32), ctx.astype(np.int32), slots.astype(np.int32)
+
+
+def argmax_rows_ref(logits: np.ndarray) -> np.ndarray:
+    """Greedy token of each row (the torch.argmax of
+    benchmarks/benchmark_engine.py:265): index of the largest value, the first
+    one among equals; a NaN ranks above every number (numpy's argmax)."""
+    return np.argmax(np.asarray(logits, dtype=np.float32), axis=-1).astype(np.int64)

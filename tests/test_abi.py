@@ -16,7 +16,7 @@ HEADER_ENTRY_POINTS = {
     "mce_paged_kv_store", "mce_paged_attention_decode_workspace_size",
     "mce_paged_attention_decode", "mce_rope_inplace", "mce_prefill_attention",
     "mce_rope_kv_store", "mce_decode_gemm", "mce_paged_attention_decode_rope",
-    "mce_rmsnorm_decode_gemm",
+    "mce_rmsnorm_decode_gemm", "mce_argmax_rows", "mce_decode_advance",
 }
 
 
@@ -181,3 +181,19 @@ def test_error_exception_carries_status(lib):
     with pytest.raises(_lib.MCEError) as ei:
         _lib.call("mce_rmsnorm", 9, None, None, None, 1, 8, 8, 8, 1e-5, None)
     assert ei.value.code == _lib.MCE_ERR_INVALID and isinstance(ei.value, RuntimeError)
+
+
+def test_decode_loop_entry_points_validate(lib):
+    f = lib.mce_argmax_rows
+    assert f(0, None, 8, 100, 100, None, None) == _lib.MCE_ERR_INVALID
+    assert "null" in _err(lib)
+    assert f(0, None, 8, 100, 50, None, None) == _lib.MCE_ERR_INVALID   # stride < cols
+    assert f(2, None, 8, 100, 100, None, None) == _lib.MCE_ERR_INVALID  # dtype
+    assert f(0, None, 0, 100, 100, None, None) == _lib.MCE_OK
+    g = lib.mce_decode_advance
+    assert g(None, None, None, None, None, None, None, 4, 8, 16, 0, None) == _lib.MCE_ERR_INVALID
+    one = ctypes.c_void_p(16)  # non-null, never dereferenced: validation fails first
+    assert g(one, one, one, one, None, one, None, 4, 8, 16, 4, None) == _lib.MCE_ERR_INVALID
+    assert "token log" in _err(lib)
+    assert g(one, one, one, one, None, None, None, 4, 8, 0, 0, None) == _lib.MCE_ERR_INVALID
+    assert g(None, None, None, None, None, None, None, 0, 8, 16, 0, None) == _lib.MCE_OK

@@ -118,3 +118,32 @@ def test_decode_crosses_block_boundary_and_block_table_width(dev):
         else:
             ref.decode(tok.cpu(), [p] * b, seq)  # keep the oracle's cache in step
             tok = out.argmax(-1, keepdim=True)
+
+
+
+def test_device_loop_matches_host_prepared_steps(dev):
+    """run_device_loop (greedy token and the next step's slots prepared on the
+    device inside the graph) generates exactly the tokens of the same steps
+    prepared on the host and replayed one by one (execute + torch.argmax)."""
+    b, s, k = 3, 45, 6
+    model, cache, _ = build(dev, b, s, k + 2)
+    ids = torch.randint(0, CFG["vocab_size"], (b, s), generator=torch.Generator().manual_seed(4))
+    seq = list(range(b))
+    logits = prefill_step(model, ids.to(dev), seq, torch.full((b,), s, dtype=torch.int32))
+    tok0 = logits.argmax(-1, keepdim=True)
+    pos0 = torch.full((b, 1), s, dtype=torch.int32, device=dev)
+    runner = CUDAGraphRunner(model, max_batch_size=b)
+    runner.capture_graph(tok0, pos0, seq, [s + 1] * b, device_steps=k)
+    dev_tokens = runner.run_device_loop(k).cpu()
+    # host-prepared replays of the same steps (their KV writes are identical)
+    tok = tok0
+    host_tokens = []
+    for i in range(k):
+        p = s + i
+        out = runner.execute(tok, torch.full((b, 1), p, dtype=torch.int32, device=dev), seq,
+                             [p + 1] * b)
+        tok = out.argmax(-1, keepdim=True)
+        host_tokens.append(tok.view(-1).cpu())
+    assert dev_tokens.tolist() == torch.stack(host_tokens).tolist()
+    with pytest.raises(RuntimeError):
+        runner.run_device_loop(k + 1)

@@ -1,11 +1,13 @@
-"""GPU parity of RMSNorm, SwiGLU, RoPE, the paged KV store and causal prefill
-attention against the CPU oracle.
+"""GPU parity of RMSNorm, SwiGLU, RoPE, the paged KV store, causal prefill
+attention, the decode-sized GEMMs and the device-side decode-loop ops against
+the CPU oracle.
 
-Bars: KV store bit-exact; RMSNorm/SwiGLU/RoPE/prefill max-abs <= 1e-2 vs the
+Bars: KV store, argmax and decode-step preparation bit-exact; RMSNorm/SwiGLU/RoPE/prefill max-abs <= 1e-2 vs the
 fp32 oracle (reference tolerance class: tests/test_ops.py:35,
 tests/test_rope.py:56-57); RMSNorm/SwiGLU/RoPE additionally within one fp16
 ulp-scale relative bound.
 """
+import numpy as np
 import pytest
 import torch
 
@@ -402,3 +404,81 @@ def test_decode_gemm_rejects_unsupported_shapes(dev):
     with pytest.raises(_lib.MCEError) as ei:
         decode_gemm(x, w)
     assert ei.value.code == _lib.MCE_ERR_UNSUPPORTED
+
+
+
+# ------------------------------------------------ device-side decode loop
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows,cols", [(8, 128256), (3, 1000), (1, 1)])
+def test_argmax_rows_matches_torch(dev, dtype, rows, cols):
+    """Greedy tokens equal torch.argmax (and the numpy oracle) exactly,
+    including rows whose maximum repeats and a row with NaNs; strided rows."""
+    from mycustomcudaengine_amd.ops import argmax_rows
+    from oracle.alloc_ref import argmax_rows_ref
+    g = gen(150 + rows)
+    buf = (torch.randn(rows, cols + 8, generator=g) * 4).to(dtype)
+    x = buf[:, :cols]
+    if cols > 10:
+        x[0, cols // 3] = x[0].max() + 1
+        x[0, cols // 2] = x[0, cols // 3]          # tie: the first wins
+        if rows > 1:
+            x[1, 5] = float("nan")
+            x[1, cols - 3] = float("nan")          # NaN ranks first, first NaN wins
+    got = argmax_rows(buf.to(dev)[:, :cols]).cpu()
+    assert got.tolist() == torch.argmax(x.float(), dim=-1).tolist()
+    assert got.tolist() == argmax_rows_ref(x.float().numpy()).tolist()
+
+
+def test_decode_advance_matches_oracle_and_replays(dev):
+    """Device-side step preparation equals the oracle step after step
+    (positions, context lengths, slots from the zero-padded table, -1 past its
+    width, the token log), eagerly and as a captured graph replayed several
+    times with host checks between the replays."""
+    from mycustomcudaengine_amd.ops import decode_advance
+    from oracle.alloc_ref import BlockAllocatorRef, decode_advance_ref
+    bs, width = 16, 5
+    a = BlockAllocatorRef(64, bs)
+    rng = np.random.default_rng(3)
+    lens = [70, 33, 16, 80]
+    for s_, n in enumerate(lens):
+        a.allocate_sequence(s_, n)
+    table = a.block_table(list(range(4)), width)
+    pos = np.array([n - 1 for n in lens], np.int32) - 3
+    ctx = pos + 1
+    d_tab = torch.from_numpy(table).to(dev)
+    d_pos, d_ctx = torch.from_numpy(pos.copy()).to(dev), torch.from_numpy(ctx.copy()).to(dev)
+    d_slot = torch.zeros(4, dtype=torch.int32, device=dev)
+    ids = torch.zeros(4, dtype=torch.int64, device=dev)
+    log = torch.full((6, 4), -7, dtype=torch.int64, device=dev)
+    ctr = torch.zeros(1, dtype=torch.int32, device=dev)
+    for step in range(3):  # eager
+        ids.copy_(torch.from_numpy(rng.integers(0, 1000, 4)))
+        want_ids = ids.cpu().clone()
+        decode_advance(d_tab, d_pos, d_ctx, d_slot, bs, input_ids=ids, token_log=log,
+                       step_counter=ctr)
+        pos, ctx, slots = decode_advance_ref(table, pos, ctx, bs)
+        assert d_pos.cpu().tolist() == pos.tolist() and d_ctx.cpu().tolist() == ctx.tolist()
+        assert d_slot.cpu().tolist() == slots.tolist()
+        assert log[step].cpu().tolist() == want_ids.tolist() and int(ctr.item()) == step + 1
+    graph = torch.cuda.CUDAGraph()
+    s_ = torch.cuda.Stream()
+    s_.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_):
+        with torch.cuda.graph(graph, stream=s_):
+            decode_advance(d_tab, d_pos, d_ctx, d_slot, bs, input_ids=ids, token_log=log,
+                           step_counter=ctr)
+    torch.cuda.current_stream().wait_stream(s_)
+    torch.cuda.synchronize()
+    for step in range(3, 8):  # replays (the log holds 6 rows: later steps are not logged)
+        ids.copy_(torch.from_numpy(rng.integers(0, 1000, 4)))
+        want_ids = ids.cpu().clone()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        pos, ctx, slots = decode_advance_ref(table, pos, ctx, bs)
+        assert d_pos.cpu().tolist() == pos.tolist() and d_ctx.cpu().tolist() == ctx.tolist()
+        assert d_slot.cpu().tolist() == slots.tolist()
+        if step < 6:
+            assert log[step].cpu().tolist() == want_ids.tolist()
+        assert int(ctr.item()) == step + 1
+    assert (slots == -1).any()  # a sequence ran past the table width

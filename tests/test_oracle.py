@@ -13,7 +13,8 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from oracle.alloc_ref import BlockAllocatorRef, prefill_slots_ref, slot_mapping_ref
+from oracle.alloc_ref import (BlockAllocatorRef, argmax_rows_ref, decode_advance_ref,
+                              prefill_slots_ref, slot_mapping_ref)
 from oracle.inputs import cfg1_decode, make_decode_case, make_prefill_case
 from oracle.ops_ref import (decode_attention_ref, gather_kv, kv_store_ref,
                             prefill_attention_ref, rmsnorm_ref, rope_ref, rope_tables,
@@ -232,3 +233,37 @@ def test_slot_rules_brute_force():
     for i, s in enumerate([0, 1]):
         for p in range(3):
             assert ps[i, p] == a.tables[s][p // 4] * 4 + p % 4
+
+
+def test_decode_advance_follows_the_allocator_slot_rule():
+    """One advance = the allocator's slot of the next position (hand-built
+    tables), -1 once the position leaves the table width; positions and
+    context lengths move by exactly one."""
+    a = BlockAllocatorRef(16, 4)
+    a.allocate_sequence(0, 10)   # blocks 0, 1, 2
+    a.allocate_sequence(1, 3)    # block 3
+    table = a.block_table([0, 1], 3)
+    pos, ctx = np.array([9, 2], np.int32), np.array([10, 3], np.int32)
+    p2, c2, sl = decode_advance_ref(table, pos, ctx, 4)
+    assert p2.tolist() == [10, 3] and c2.tolist() == [11, 4]
+    assert sl.tolist() == [a.tables[0][2] * 4 + 2, a.tables[1][0] * 4 + 3]
+    # sequence 1 moves into its (zero-padded) second table entry, sequence 0 past the width
+    p3, c3, sl3 = decode_advance_ref(table, [11, 3], [12, 4], 4)
+    assert sl3.tolist() == [-1, 0 * 4 + 0]
+    # agrees with slot_mapping_ref wherever the table has the block
+    for step in range(6):
+        q = np.array([2 + step, 1 + step], np.int32)
+        _, cn, s_ = decode_advance_ref(table, q, q + 1, 4)
+        want = slot_mapping_ref(a.tables, [0, 1], cn, 4) if cn[1] <= 4 else None
+        if want is not None:
+            assert s_.tolist() == want.tolist()
+
+
+def test_argmax_rows_ref_tie_and_nan_rules():
+    x = np.array([[1.0, 3.0, 3.0, -2.0],     # first of equal maxima
+                  [-np.inf, -np.inf, -5.0, -5.0],
+                  [0.0, np.nan, 7.0, np.nan],  # NaN above every number, first NaN
+                  [2.0, 2.0, 2.0, 2.0]], np.float32)
+    got = argmax_rows_ref(x)
+    assert got.tolist() == [1, 2, 1, 0]
+    assert got.tolist() == torch.argmax(torch.from_numpy(x), dim=-1).tolist()
