@@ -280,6 +280,29 @@ MCE_API int mce_prefill_attention(int dtype, const void *query, const void *key,
                           int seq_len, int num_heads, int num_kv_heads,
                           int head_dim, float scale, void *stream);
 
+/*
+ * Chunked causal prefill attention with K/V from the page pool: query
+ * [batch, seq_len, num_heads, 128] holds the last seq_len positions of each
+ * sequence; sequence b has context_lens[b] tokens (clamped into [seq_len,
+ * max_blocks_per_seq * block_size]) whose K/V rows are in key_cache /
+ * value_cache [num_blocks, block_size, num_kv_heads, 128] at the slots of
+ * block_tables[b] (int32 [batch, max_blocks_per_seq], block ids clamped into
+ * the pool).  Query i of sequence b is position context_lens[b] - seq_len + i
+ * and attends causally to keys 0 .. that position; output like query.  The
+ * pool must be smaller than 2 GiB, max_blocks_per_seq <= 8192.  With
+ * context_lens == seq_len and an identity table it equals
+ * mce_prefill_attention on the same K/V bit for bit.  Widens the reference's
+ * prefill (benchmarks/benchmark_engine.py:64-89 with
+ * csrc/kernels/prefill_attention.cu:271-309: contiguous K/V of the whole
+ * prompt) to prompts processed in chunks against the cached prefix.
+ */
+MCE_API int mce_prefill_attention_paged(int dtype, const void *query, const void *key_cache,
+                                        const void *value_cache, const int32_t *block_tables,
+                                        const int32_t *context_lens, void *output, int batch,
+                                        int seq_len, int num_heads, int num_kv_heads,
+                                        int head_dim, int max_blocks_per_seq, int block_size,
+                                        int64_t num_blocks, float scale, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

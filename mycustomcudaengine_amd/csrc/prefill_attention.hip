@@ -100,10 +100,19 @@ __device__ __forceinline__ float xor32_add(float x) {
 struct PrefillArgs {
   const uint16_t *q, *k, *v;
   uint16_t *out;
-  int B, S, Hq, Hkv, G;
+  int B, S, Hq, Hkv, G;  // S: query rows (positions) per sequence
   int n_items;
   float scale_log2;
+  // paged mode: K / V rows from the page pool [num_blocks, bs, Hkv, 128]
+  // through block_tables [B, maxb]; sequence b has ctx_b = context_lens[b]
+  // keys and its S queries are its last S positions (ctx_b - S ..).
+  const int32_t *block_tables, *context_lens;
+  int maxb, bs_log2;
+  int64_t num_blocks;
+  uint32_t cache_bytes;  // bytes of one cache (< 2^31)
 };
+
+constexpr int PF_MAX_BLOCKS = 8192;  // paged mode: block-table row staged in LDS
 
 // NRB row blocks of 32 rows per workgroup and KSPLIT key streams: wave w owns
 // row block w % NRB and key stream kh = w / NRB, which takes key tiles kh,
@@ -112,7 +121,11 @@ struct PrefillArgs {
 // halved; the streams keep separate online-softmax states that are merged
 // through LDS at the end.  KSPLIT = 1 suits grids with several workgroups
 // per CU, where the co-resident workgroups already fill the SIMDs.
-template <class T, int NRB, int KSPLIT>
+//
+// PAGED: K / V come from the page pool (chunked prefill: the queries are the
+// last S positions of each sequence and attend to all its cached keys); the
+// contiguous mode is PAGED = false with ctx_b = S.
+template <class T, int NRB, int KSPLIT, bool PAGED>
 __global__ __launch_bounds__(NRB * KSPLIT * 64) __attribute__((amdgpu_waves_per_eu(PF_WAVES_PER_EU, PF_WAVES_PER_EU)))
 void prefill_causal_kernel(PrefillArgs a) {
   constexpr int BM = 32 * NRB;
@@ -143,6 +156,11 @@ void prefill_causal_kernel(PrefillArgs a) {
   const int b = (id / a.Hkv) % a.B;
   const int item_rank = id / (a.Hkv * a.B);
   const int G = a.G, S = a.S;
+  // keys of this sequence and the position of its first query row
+  const int cap_keys = PAGED ? min(a.maxb << a.bs_log2, 1 << 30) : S;
+  const int key_S = PAGED ? min(max(a.context_lens[b], S), cap_keys) : S;
+  const int p0 = key_S - S;
+  __shared__ int bt_lds[PAGED ? PF_MAX_BLOCKS : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -154,8 +172,19 @@ void prefill_causal_kernel(PrefillArgs a) {
 
   const int64_t q_row_stride = (int64_t)a.Hq * PF_HD;
   const int kv_row = a.Hkv * PF_HD;  // elements between consecutive keys
-  const uint16_t *kbase = a.k + ((int64_t)b * S * a.Hkv + g) * PF_HD;
-  const uint16_t *vbase = a.v + ((int64_t)b * S * a.Hkv + g) * PF_HD;
+  const uint16_t *kbase = PAGED ? a.k + (int64_t)g * PF_HD : a.k + ((int64_t)b * S * a.Hkv + g) * PF_HD;
+  const uint16_t *vbase = PAGED ? a.v + (int64_t)g * PF_HD : a.v + ((int64_t)b * S * a.Hkv + g) * PF_HD;
+  if constexpr (PAGED) {
+    // byte offset in the pool of each of the sequence's pages (block ids
+    // clamped into the pool), before any K / V load
+    const int32_t *btr = a.block_tables + (int64_t)b * a.maxb;
+    const int nb_hi = (int)min(a.num_blocks - 1, (int64_t)0x7fffffff);
+    for (int i = tid; i < a.maxb; i += NRB * KSPLIT * 64) {
+      const int v = btr[i];
+      bt_lds[i] = ((v < 0 ? 0 : (v > nb_hi ? nb_hi : v)) << a.bs_log2) * kv_row * 2;
+    }
+    lds_barrier();
+  }
   const float c = a.scale_log2;
 
   // Per-thread staging assignments within a key stream (fixed for the kernel):
@@ -166,7 +195,9 @@ void prefill_causal_kernel(PrefillArgs a) {
   // stores) with loop-invariant per-thread offsets; the hardware range check
   // of the buffer descriptor returns zeros for keys at or past the sequence
   // end (the descriptor spans this (batch, kv head)'s rows up to key S).
-  const int kv_bytes = (S * kv_row - g * PF_HD) * 2;
+  // (paged: the descriptor spans the whole pool; keys past the sequence end
+  // are clamped to its last key, which the causal mask hides)
+  const int kv_bytes = PAGED ? (int)(a.cache_bytes - g * PF_HD * 2) : (S * kv_row - g * PF_HD) * 2;
   const __amdgpu_buffer_rsrc_t krsrc =
       __builtin_amdgcn_make_buffer_rsrc((void *)kbase, (short)0, kv_bytes, BUF_RSRC_WORD3);
   const __amdgpu_buffer_rsrc_t vrsrc =
@@ -175,8 +206,16 @@ void prefill_causal_kernel(PrefillArgs a) {
 #pragma unroll
   for (int it = 0; it < KP; ++it) {
     const int pc = tid_h + it * NT;
-    kv_voff[it] = ((pc >> 4) * kv_row + (pc & 15) * 8) * 2;
+    kv_voff[it] = PAGED ? (pc & 15) * 8 * 2 : ((pc >> 4) * kv_row + (pc & 15) * 8) * 2;
   }
+  // paged mode: byte offset in the pool of piece it of stream tile u (the
+  // pieces of a thread share their column and lie NT / 16 keys apart)
+  const int bsm = (1 << a.bs_log2) - 1;
+  const int pkey = tid_h >> 4, pcol = (tid_h & 15) * 16;
+  auto paged_off = [&](int u, int it) {
+    const int key = min((KSPLIT * u + kh) * PF_BN + pkey + it * (NT / 16), key_S - 1);
+    return bt_lds[key >> a.bs_log2] + (key & bsm) * kv_row * 2 + pcol;
+  };
   // stream index u of this key stream <-> key tile KSPLIT u + kh
   // (wave-uniform, passed as the scalar offset of the buffer loads)
   auto tile_off = [&](int u) {
@@ -187,18 +226,32 @@ void prefill_causal_kernel(PrefillArgs a) {
   KRegs kreg[2];
   VRegs vreg[2];
   auto load_k = [&](KRegs &dst, int u) {
-    const int off = tile_off(u);
+    if constexpr (PAGED) {
 #pragma unroll
-    for (int it = 0; it < KP; ++it)
-      dst[it] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(krsrc, kv_voff[it], off, 0));
+      for (int it = 0; it < KP; ++it)
+        dst[it] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(krsrc, paged_off(u, it), 0, 0));
+    } else {
+      const int off = tile_off(u);
+#pragma unroll
+      for (int it = 0; it < KP; ++it)
+        dst[it] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(krsrc, kv_voff[it], off, 0));
+    }
   };
   auto load_v = [&](VRegs &dst, int u) {
-    const int off = tile_off(u);
+    if constexpr (PAGED) {
 #pragma unroll
-    for (int it = 0; it < KP; ++it)
-      dst[it] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrsrc, kv_voff[it], off, 0));
+      for (int it = 0; it < KP; ++it)
+        dst[it] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrsrc, paged_off(u, it), 0, 0));
+    } else {
+      const int off = tile_off(u);
+#pragma unroll
+      for (int it = 0; it < KP; ++it)
+        dst[it] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrsrc, kv_voff[it], off, 0));
+    }
   };
   auto store_k = [&](const KRegs &src, uint16_t *ks) {
 #pragma unroll
@@ -220,20 +273,21 @@ void prefill_causal_kernel(PrefillArgs a) {
   const int r_item = item * BM;
   const int r_wave = r_item + 32 * rb;
   const int row = r_wave + r32;                 // this lane's row
-  const int pos = row / G, h = g * G + (row - pos * G);
+  const int qi = row / G, h = g * G + (row - qi * G);
+  const int pos = p0 + qi;                      // its position among the keys
   const bool row_ok = row < rows_total;
-  const int wave_min_pos = r_wave / G;
-  const int item_max_pos = min(S - 1, (r_item + BM - 1) / G);
+  const int wave_min_pos = p0 + r_wave / G;
+  const int item_max_pos = p0 + min(S - 1, (r_item + BM - 1) / G);
   const int n_ktiles = item_max_pos / PF_BN + 1;  // key tiles of the item
   // iterations per key stream, rounded up to even for the ping-pong unroll
   const int n_iter = ((n_ktiles + KSPLIT - 1) / KSPLIT + 1) / 2 * 2;
   // key tiles this wave's rows need (none for a block of padding rows)
   const int n_wtiles =
-      r_wave < rows_total ? min(S - 1, min(r_wave + 31, rows_total - 1) / G) / PF_BN + 1 : 0;
+      r_wave < rows_total ? (p0 + min(S - 1, min(r_wave + 31, rows_total - 1) / G)) / PF_BN + 1 : 0;
   // tiles [0, n_full) need no mask for this wave: every key <= its first
-  // position and < S
-  const int n_full = min((wave_min_pos + 1) / PF_BN, S / PF_BN);
-  const int lim = min(pos, S - 1) - 4 * hf;  // masked tiles: key offset limit + n0
+  // position and < key_S
+  const int n_full = min((wave_min_pos + 1) / PF_BN, key_S / PF_BN);
+  const int lim = min(pos, key_S - 1) - 4 * hf;  // masked tiles: key offset limit + n0
 
   // Q^T as MFMA B operand: lane supplies Q[pos, h][16 i + 8 hf + j], for fp16
   // pre-scaled by c (so the accumulators come out in log2 units); bf16 keeps
@@ -246,7 +300,7 @@ void prefill_causal_kernel(PrefillArgs a) {
   // sets follow once K_0 is staged.
   u32x4 qreg[8];
   {
-    const uint16_t *qp = a.q + ((int64_t)b * S + (row_ok ? pos : 0)) * q_row_stride +
+    const uint16_t *qp = a.q + ((int64_t)b * S + (row_ok ? qi : 0)) * q_row_stride +
                          (int64_t)(row_ok ? h : 0) * PF_HD + 8 * hf;
 #pragma unroll
     for (int i = 0; i < 8; ++i) qreg[i] = *reinterpret_cast<const u32x4 *>(qp + 16 * i);
@@ -558,6 +612,38 @@ void prefill_causal_kernel(PrefillArgs a) {
 
 using namespace mce;
 
+namespace {
+
+// Items of 128 rows per (batch, kv head), heaviest first: when there are more
+// items than workgroup slots, the dispatcher hands the lighter ones to the
+// CUs that free up first (longest-processing-time-first scheduling).  The
+// key range is split over two wave sets when the grid alone would not give
+// every CU about two workgroups (long causal sequences, small batch).
+constexpr int PF_NRB = 4;
+
+template <bool PAGED>
+int prefill_launch(int dtype, PrefillArgs &a, void *stream, const char *name) {
+  a.n_items = (int)(((int64_t)a.S * a.G + 32 * PF_NRB - 1) / (32 * PF_NRB));
+  const int64_t grid = (int64_t)a.n_items * a.B * a.Hkv;
+  MCE_REQUIRE(grid < ((int64_t)1 << 31), "%s: problem too large", name);
+  hipStream_t st = (hipStream_t)stream;
+  const bool split = grid < 2 * (int64_t)cu_count();
+  if (dtype == MCE_F16) {
+    if (split)
+      prefill_causal_kernel<F16T, PF_NRB, 2, PAGED><<<(unsigned)grid, PF_NRB * 128, 0, st>>>(a);
+    else
+      prefill_causal_kernel<F16T, PF_NRB, 1, PAGED><<<(unsigned)grid, PF_NRB * 64, 0, st>>>(a);
+  } else {
+    if (split)
+      prefill_causal_kernel<BF16T, PF_NRB, 2, PAGED><<<(unsigned)grid, PF_NRB * 128, 0, st>>>(a);
+    else
+      prefill_causal_kernel<BF16T, PF_NRB, 1, PAGED><<<(unsigned)grid, PF_NRB * 64, 0, st>>>(a);
+  }
+  return check_launch(name);
+}
+
+}  // namespace
+
 extern "C" int mce_prefill_attention(int dtype, const void *query,
                                      const void *key, const void *value,
                                      void *output, int batch, int seq_len,
@@ -584,12 +670,6 @@ extern "C" int mce_prefill_attention(int dtype, const void *query,
   // (including the prefetch of up to 5 tiles past the end)
   MCE_REQUIRE(((int64_t)seq_len + 256) * num_kv_heads * head_dim * 2 < ((int64_t)1 << 31),
               "mce_prefill_attention: seq_len * num_kv_heads too large");
-  // Items of 128 rows, one per workgroup, heaviest first: when there are more
-  // items than workgroup slots, the dispatcher hands the lighter ones to the
-  // CUs that free up first (longest-processing-time-first scheduling).
-  constexpr int nrb = 4;
-  // Split the key range over two wave sets when the grid alone would not
-  // give every CU about two workgroups (long causal sequences, small batch).
   PrefillArgs a{};
   a.q = (const uint16_t *)query;
   a.k = (const uint16_t *)key;
@@ -600,22 +680,61 @@ extern "C" int mce_prefill_attention(int dtype, const void *query,
   a.Hq = num_heads;
   a.Hkv = num_kv_heads;
   a.G = G;
-  a.n_items = (int)(((int64_t)seq_len * G + 32 * nrb - 1) / (32 * nrb));
   a.scale_log2 = scale * 1.4426950408889634f;
-  const int64_t grid = (int64_t)a.n_items * batch * num_kv_heads;
-  MCE_REQUIRE(grid < ((int64_t)1 << 31), "mce_prefill_attention: problem too large");
-  hipStream_t st = (hipStream_t)stream;
-  const bool split = grid < 2 * (int64_t)cu_count();
-  if (dtype == MCE_F16) {
-    if (split)
-      prefill_causal_kernel<F16T, nrb, 2><<<(unsigned)grid, nrb * 128, 0, st>>>(a);
-    else
-      prefill_causal_kernel<F16T, nrb, 1><<<(unsigned)grid, nrb * 64, 0, st>>>(a);
-  } else {
-    if (split)
-      prefill_causal_kernel<BF16T, nrb, 2><<<(unsigned)grid, nrb * 128, 0, st>>>(a);
-    else
-      prefill_causal_kernel<BF16T, nrb, 1><<<(unsigned)grid, nrb * 64, 0, st>>>(a);
-  }
-  return check_launch("mce_prefill_attention");
+  return prefill_launch<false>(dtype, a, stream, "mce_prefill_attention");
+}
+
+extern "C" int mce_prefill_attention_paged(int dtype, const void *query, const void *key_cache,
+                                           const void *value_cache, const int32_t *block_tables,
+                                           const int32_t *context_lens, void *output, int batch,
+                                           int seq_len, int num_heads, int num_kv_heads,
+                                           int head_dim, int max_blocks_per_seq, int block_size,
+                                           int64_t num_blocks, float scale, void *stream) {
+  clear_error();
+  const char *name = "mce_prefill_attention_paged";
+  MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16, "%s: unknown dtype %d", name, dtype);
+  MCE_REQUIRE(head_dim == PF_HD, "%s: head_dim must be 128 (got %d)", name, head_dim);
+  MCE_REQUIRE(batch >= 0 && seq_len >= 0 && num_heads >= 1 && num_kv_heads >= 1 &&
+                  max_blocks_per_seq >= 0 && num_blocks >= 0,
+              "%s: bad shape", name);
+  MCE_REQUIRE(num_heads % num_kv_heads == 0, "%s: num_heads %d not a multiple of num_kv_heads %d",
+              name, num_heads, num_kv_heads);
+  MCE_REQUIRE(is_pow2(block_size) && block_size >= 1 && block_size <= 1024,
+              "%s: block_size must be a power of two <= 1024 (got %d)", name, block_size);
+  if (batch == 0 || seq_len == 0) return MCE_OK;
+  MCE_REQUIRE(query && key_cache && value_cache && block_tables && context_lens && output,
+              "%s: null pointer", name);
+  MCE_REQUIRE(aligned16(query) && aligned16(key_cache) && aligned16(value_cache) &&
+                  aligned16(output),
+              "%s: tensors must be 16-byte aligned", name);
+  MCE_REQUIRE(max_blocks_per_seq <= PF_MAX_BLOCKS,
+              "%s: at most %d blocks per sequence (got %d)", name, PF_MAX_BLOCKS,
+              max_blocks_per_seq);
+  MCE_REQUIRE((int64_t)max_blocks_per_seq * block_size >= seq_len,
+              "%s: the block tables hold %lld tokens, fewer than the %d query positions", name,
+              (long long)max_blocks_per_seq * block_size, seq_len);
+  MCE_REQUIRE(num_blocks >= 1, "%s: empty page pool", name);
+  const int G = num_heads / num_kv_heads;
+  MCE_REQUIRE((int64_t)seq_len * G < ((int64_t)1 << 30), "%s: too many query rows", name);
+  const int64_t cache_bytes = num_blocks * block_size * num_kv_heads * head_dim * 2;
+  MCE_REQUIRE(cache_bytes < ((int64_t)1 << 31),
+              "%s: the page pool must be smaller than 2 GiB (32-bit offsets)", name);
+  PrefillArgs a{};
+  a.q = (const uint16_t *)query;
+  a.k = (const uint16_t *)key_cache;
+  a.v = (const uint16_t *)value_cache;
+  a.out = (uint16_t *)output;
+  a.B = batch;
+  a.S = seq_len;
+  a.Hq = num_heads;
+  a.Hkv = num_kv_heads;
+  a.G = G;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.block_tables = block_tables;
+  a.context_lens = context_lens;
+  a.maxb = max_blocks_per_seq;
+  a.bs_log2 = ilog2(block_size);
+  a.num_blocks = num_blocks;
+  a.cache_bytes = (uint32_t)cache_bytes;
+  return prefill_launch<true>(dtype, a, stream, name);
 }

@@ -509,3 +509,44 @@ def prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tenso
         _lib.call("mce_prefill_attention", code, q.data_ptr(), k.data_ptr(), v.data_ptr(),
                   out.data_ptr(), b, s, hq, hkv, d, float(scale), _stream(dev))
     return out
+
+
+def prefill_attention_paged(query: torch.Tensor, key_cache: torch.Tensor,
+                            value_cache: torch.Tensor, block_tables: torch.Tensor,
+                            context_lens: torch.Tensor, scale: float) -> torch.Tensor:
+    """Chunked causal prefill attention reading K/V from the page pool.
+
+    query [B, S, Hq, D] holds the last S positions of each sequence; sequence
+    b has context_lens[b] (>= S) tokens whose K/V are already in the caches
+    ([num_blocks, block_size, Hkv, D], e.g. written by rope_kv_store) at the
+    slots block_tables[b] ([B, W] int32) gives.  Query i of sequence b sits at
+    position context_lens[b] - S + i and attends to keys 0 .. that position.
+    Returns [B, S, Hq, D].  Widens the reference's prefill
+    (benchmarks/benchmark_engine.py:64-89, contiguous K/V of the whole prompt)
+    to prompts processed in chunks against the cached prefix."""
+    dev = _on_gpu("prefill_attention_paged", query, key_cache, value_cache, block_tables,
+                  context_lens)
+    code = _dtype_code(query, "prefill_attention_paged query")
+    _check(key_cache.dtype == query.dtype and value_cache.dtype == query.dtype,
+           "prefill_attention_paged: cache dtype must match query")
+    _check(query.dim() == 4 and key_cache.dim() == 4 and value_cache.shape == key_cache.shape
+           and key_cache.is_contiguous() and value_cache.is_contiguous(),
+           "prefill_attention_paged: expected query [B, S, Hq, D] and contiguous caches "
+           "[num_blocks, block_size, Hkv, D]")
+    b, s, hq, d = query.shape
+    nb, bs, hkv, dk = key_cache.shape
+    _check(dk == d, "prefill_attention_paged: head_dim of query and caches differ")
+    _check(block_tables.dtype == torch.int32 and block_tables.dim() == 2 and
+           block_tables.size(0) == b and block_tables.is_contiguous(),
+           f"prefill_attention_paged: block_tables must be contiguous int32 [{b}, W]")
+    _check(context_lens.dtype == torch.int32 and context_lens.numel() == b and
+           context_lens.is_contiguous(),
+           f"prefill_attention_paged: context_lens must be {b} contiguous int32 values")
+    q = query if query.is_contiguous() else query.contiguous()
+    out = torch.empty_like(q)
+    with _on_device(dev):
+        _lib.call("mce_prefill_attention_paged", code, q.data_ptr(), key_cache.data_ptr(),
+                  value_cache.data_ptr(), block_tables.data_ptr(), context_lens.data_ptr(),
+                  out.data_ptr(), b, s, hq, hkv, d, block_tables.size(1), bs, nb, float(scale),
+                  _stream(dev))
+    return out

@@ -151,3 +151,20 @@ def prefill_attention_ref(query: torch.Tensor, key: torch.Tensor, value: torch.T
 def scale_for(head_dim: int) -> float:
     """1 / sqrt(head_dim) (engine/models/llama.py:38)."""
     return 1.0 / math.sqrt(head_dim)
+
+
+def prefill_paged_ref(query: torch.Tensor, key_cache: torch.Tensor, value_cache: torch.Tensor,
+                      block_table_row, ctx: int, scale: float) -> torch.Tensor:
+    """Chunked causal prefill of one sequence from the page pool: query
+    [S, Hq, D] holds positions ctx - S .. ctx - 1; K/V of positions 0 .. ctx-1
+    are gathered through the block table (gather_kv) and row i attends to
+    keys 0 .. ctx - S + i.  Returns [S, Hq, D] fp32.  Causal attention of
+    the whole sequence (prefill_attention_ref) restricted to its last S rows:
+    a row depends on its own query and the keys up to its position only, so
+    the earlier positions' queries are zeros here."""
+    s, hq, d = query.shape
+    k = gather_kv(key_cache, block_table_row, ctx)
+    v = gather_kv(value_cache, block_table_row, ctx)
+    q = torch.zeros(ctx, hq, d, dtype=query.dtype)
+    q[ctx - s:] = query
+    return prefill_attention_ref(q[None], k[None], v[None], scale)[0, ctx - s:]

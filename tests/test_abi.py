@@ -17,6 +17,7 @@ HEADER_ENTRY_POINTS = {
     "mce_paged_attention_decode", "mce_rope_inplace", "mce_prefill_attention",
     "mce_rope_kv_store", "mce_decode_gemm", "mce_paged_attention_decode_rope",
     "mce_rmsnorm_decode_gemm", "mce_argmax_rows", "mce_decode_advance",
+    "mce_prefill_attention_paged",
 }
 
 
@@ -197,3 +198,24 @@ def test_decode_loop_entry_points_validate(lib):
     assert "token log" in _err(lib)
     assert g(one, one, one, one, None, None, None, 4, 8, 0, 0, None) == _lib.MCE_ERR_INVALID
     assert g(None, None, None, None, None, None, None, 0, 8, 16, 0, None) == _lib.MCE_OK
+
+
+def test_prefill_paged_validation(lib):
+    f = lib.mce_prefill_attention_paged
+    one = ctypes.c_void_p(16)  # non-null, never dereferenced: validation fails first
+    args = [0, one, one, one, one, one, one, 2, 64, 24, 8, 128, 8, 16, 64, 0.1, None]
+    # (args itself is valid and would launch: only invalid variants are called)
+    bad = list(args); bad[11] = 64
+    assert f(*bad) == _lib.MCE_ERR_INVALID and "head_dim" in _err(lib)
+    bad = list(args); bad[13] = 12
+    assert f(*bad) == _lib.MCE_ERR_INVALID and "power of two" in _err(lib)
+    bad = list(args); bad[12] = 3   # 3 blocks x 16 tokens < 64 query positions
+    assert f(*bad) == _lib.MCE_ERR_INVALID and "fewer than" in _err(lib)
+    bad = list(args); bad[12] = 9000
+    assert f(*bad) == _lib.MCE_ERR_INVALID and "8192" in _err(lib)
+    bad = list(args); bad[1] = None
+    assert f(*bad) == _lib.MCE_ERR_INVALID and "null" in _err(lib)
+    bad = list(args); bad[14] = 1 << 20   # pool of 4 GiB
+    assert f(*bad) == _lib.MCE_ERR_INVALID and "2 GiB" in _err(lib)
+    empty = list(args); empty[8] = 0
+    assert f(*empty) == _lib.MCE_OK

@@ -14,8 +14,8 @@ import torch
 import my_cuda_engine_cpp as ops
 from oracle.alloc_ref import BlockAllocatorRef, prefill_slots_ref
 from oracle.inputs import cfg3_prefill, make_prefill_case
-from oracle.ops_ref import (kv_store_ref, prefill_attention_ref, rmsnorm_ref, rope_ref,
-                            rope_tables, swiglu_ref)
+from oracle.ops_ref import (kv_store_ref, prefill_attention_ref, prefill_paged_ref, rmsnorm_ref,
+                            rope_ref, rope_tables, swiglu_ref)
 
 TOL = 1e-2
 pytestmark = pytest.mark.gpu
@@ -482,3 +482,66 @@ def test_decode_advance_matches_oracle_and_replays(dev):
             assert log[step].cpu().tolist() == want_ids.tolist()
         assert int(ctr.item()) == step + 1
     assert (slots == -1).any()  # a sequence ran past the table width
+
+
+
+# ------------------------------------------------ chunked prefill from the page pool
+def _paged_case(seed, prefixes, s, dtype=torch.float16, hq=24, hkv=8, bs=16):
+    """Per-sequence prefix lengths, chunk of s queries; a shuffled pool whose
+    unused pages hold NaN (a read outside the tables would poison rows)."""
+    g = gen(seed)
+    b = len(prefixes)
+    ctx = [p_ + s for p_ in prefixes]
+    width = max((c + bs - 1) // bs for c in ctx) + 1
+    nb = b * width + 5
+    kc = torch.full((nb, bs, hkv, 128), float("nan"), dtype=dtype)
+    vc = torch.full((nb, bs, hkv, 128), float("nan"), dtype=dtype)
+    perm = torch.randperm(nb, generator=g)
+    table = torch.zeros(b, width, dtype=torch.int32)
+    for i in range(b):
+        blocks = perm[i * width:(i + 1) * width]
+        table[i] = blocks.to(torch.int32)
+        used = (ctx[i] + bs - 1) // bs
+        kc[blocks[:used]] = torch.randn(used, bs, hkv, 128, generator=g).to(dtype)
+        vc[blocks[:used]] = torch.randn(used, bs, hkv, 128, generator=g).to(dtype)
+    q = torch.randn(b, s, hq, 128, generator=g).to(dtype)
+    return q, kc, vc, table, torch.tensor(ctx, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("prefixes,s,dtype", [([0, 37], 64, torch.float16),
+                                              ([100, 5, 300], 17, torch.float16),
+                                              ([700], 1, torch.float16),
+                                              ([129], 300, torch.float16),
+                                              ([2000], 48, torch.float16),
+                                              ([0, 64], 96, torch.bfloat16)])
+def test_prefill_paged_matches_oracle(dev, prefixes, s, dtype):
+    from mycustomcudaengine_amd.ops import prefill_attention_paged
+    q, kc, vc, table, ctx = _paged_case(160 + s + len(prefixes), prefixes, s, dtype)
+    scale = 1.0 / 128 ** 0.5
+    out = prefill_attention_paged(q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), ctx.to(dev),
+                                  scale).cpu()
+    assert not torch.isnan(out).any()
+    for i in range(len(prefixes)):
+        ref = prefill_paged_ref(q[i], kc, vc, table[i].tolist(), int(ctx[i]), scale)
+        err = (out[i].float() - ref).abs().max().item()
+        assert err <= TOL, (i, err)
+
+
+@pytest.mark.parametrize("b,s", [(1, 2048), (2, 333), (8, 512)])
+def test_prefill_paged_without_prefix_equals_contiguous(dev, b, s):
+    """No cached prefix (context == chunk): the paged kernel gives exactly the
+    bits of mce_prefill_attention on the same K/V laid out contiguously."""
+    from mycustomcudaengine_amd.ops import prefill_attention_paged
+    q, kc, vc, table, ctx = _paged_case(170 + b, [0] * b, s)
+    k = torch.stack([gather_kv_rows(kc, table[i], s) for i in range(b)])
+    v = torch.stack([gather_kv_rows(vc, table[i], s) for i in range(b)])
+    scale = 1.0 / 128 ** 0.5
+    paged = prefill_attention_paged(q.to(dev), kc.to(dev), vc.to(dev), table.to(dev),
+                                    ctx.to(dev), scale)
+    contig = ops.prefill_attention(q.to(dev), k.to(dev), v.to(dev), scale)
+    assert torch.equal(paged.view(torch.int16), contig.view(torch.int16))
+
+
+def gather_kv_rows(cache, row, n):
+    from oracle.ops_ref import gather_kv
+    return gather_kv(cache, row.tolist(), n)

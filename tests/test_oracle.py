@@ -16,7 +16,7 @@ import torch.nn.functional as F
 from oracle.alloc_ref import (BlockAllocatorRef, argmax_rows_ref, decode_advance_ref,
                               prefill_slots_ref, slot_mapping_ref)
 from oracle.inputs import cfg1_decode, make_decode_case, make_prefill_case
-from oracle.ops_ref import (decode_attention_ref, gather_kv, kv_store_ref,
+from oracle.ops_ref import (decode_attention_ref, gather_kv, kv_store_ref, prefill_paged_ref,
                             prefill_attention_ref, rmsnorm_ref, rope_ref, rope_tables,
                             swiglu_ref)
 
@@ -267,3 +267,23 @@ def test_argmax_rows_ref_tie_and_nan_rules():
     got = argmax_rows_ref(x)
     assert got.tolist() == [1, 2, 1, 0]
     assert got.tolist() == torch.argmax(torch.from_numpy(x), dim=-1).tolist()
+
+
+def test_prefill_paged_ref_is_the_tail_of_the_full_prefill():
+    """The chunked restatement equals the last rows of the whole-sequence
+    causal prefill whatever the earlier rows' queries are (causality), on a
+    shuffled page pool, and with no prefix it is the whole prefill."""
+    g = torch.Generator().manual_seed(9)
+    bs, nb, hq, hkv, d = 4, 12, 4, 2, 16
+    kc = torch.randn(nb, bs, hkv, d, generator=g)
+    vc = torch.randn(nb, bs, hkv, d, generator=g)
+    table = torch.randperm(nb, generator=g)[:6].tolist()
+    ctx, s = 19, 5
+    q_all = torch.randn(ctx, hq, d, generator=g)
+    k = gather_kv(kc, table, ctx)
+    v = gather_kv(vc, table, ctx)
+    full = prefill_attention_ref(q_all[None], k[None], v[None], 0.3)[0]
+    got = prefill_paged_ref(q_all[ctx - s:], kc, vc, table, ctx, 0.3)
+    assert torch.allclose(got, full[ctx - s:], atol=1e-6)
+    whole = prefill_paged_ref(q_all, kc, vc, table, ctx, 0.3)
+    assert torch.allclose(whole, full, atol=1e-6)
