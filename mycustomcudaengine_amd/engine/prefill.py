@@ -15,6 +15,13 @@ output with a stray transpose (:90-91) and computes an unused GQA expansion
 tables in one host->device copy and the attention output is used as
 [B, S, Hq * D] directly.  The sequences must already own blocks for S tokens
 (KVCacheManager.allocate_sequence), as in the reference.
+
+With chunk_size < S the prompt is processed chunk_size positions at a time:
+each chunk's K/V go to the page pool first and its queries attend to every
+cached key so far through ops.prefill_attention_paged, so activations scale
+with the chunk, not the prompt; the cache holds the same slots as after the
+one-shot prefill and cache and logits agree within rounding (the library GEMM
+may choose another kernel for the chunk's row count).
 """
 from __future__ import annotations
 
@@ -24,13 +31,15 @@ import torch
 
 import my_cuda_engine_cpp as ops
 
-from ..ops import rope_kv_store
+from ..ops import prefill_attention_paged, rope_kv_store
 
 
 def prefill_step(model, input_ids: torch.Tensor, seq_ids: List[int],
-                 context_lens: torch.Tensor = None) -> torch.Tensor:
+                 context_lens: torch.Tensor = None, chunk_size: int = None) -> torch.Tensor:
     c = model.config
     b, s = input_ids.shape
+    if chunk_size is not None and 0 < chunk_size < s:
+        return _prefill_chunked(model, input_ids, seq_ids, chunk_size)
     hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
     dev = input_ids.device
     cache = model.cache_manager
@@ -50,5 +59,40 @@ def prefill_step(model, input_ids: torch.Tensor, seq_ids: List[int],
         x.addmm_(attn.view(b * s, hq * d), model.weights[f"{p}.self_attn.o_proj.weight"].T)
         model._mlp(l, x)
     last = x.view(b, s, -1)[:, -1].contiguous()
+    xf = ops.rmsnorm(last, model.weights["model.norm.weight"], c.rms_norm_eps)
+    return torch.matmul(xf, model.lm_head.T)
+
+
+def _prefill_chunked(model, input_ids: torch.Tensor, seq_ids: List[int],
+                     chunk: int) -> torch.Tensor:
+    c = model.config
+    b, s = input_ids.shape
+    hq, hkv, d = c.num_attention_heads, c.num_key_value_heads, c.head_dim
+    dev = input_ids.device
+    cache = model.cache_manager
+    all_slots = torch.from_numpy(cache.prefill_slot_mapping(seq_ids, s)).to(dev).view(b, s)
+    width = (s + cache.block_size - 1) // cache.block_size
+    tables = cache.get_block_table_tensor(seq_ids, width)
+    kv = cache.kv_cache
+    x = None
+    for c0 in range(0, s, chunk):
+        c1 = min(s, c0 + chunk)
+        n = c1 - c0
+        slots = all_slots[:, c0:c1].contiguous().view(-1)
+        positions = torch.arange(c0, c1, dtype=torch.int32, device=dev).repeat(b, 1).contiguous()
+        ctx = torch.full((b,), c1, dtype=torch.int32, device=dev)
+        x = model.weights["model.embed_tokens.weight"][input_ids[:, c0:c1].reshape(-1)]
+        for l in range(c.num_hidden_layers):
+            p = f"model.layers.{l}"
+            xn = ops.rmsnorm(x, model.weights[f"{p}.input_layernorm.weight"], c.rms_norm_eps)
+            q, k, v = model._attention_block_proj(l, xn)
+            rope_kv_store(q.view(b * n, hq, d), k.view(b * n, hkv, d), v.view(b * n, hkv, d),
+                          kv[l, 0], kv[l, 1], model.cos_table, model.sin_table,
+                          positions.view(-1), slots)
+            attn = prefill_attention_paged(q.view(b, n, hq, d), kv[l, 0], kv[l, 1], tables, ctx,
+                                           model.scale)
+            x.addmm_(attn.view(b * n, hq * d), model.weights[f"{p}.self_attn.o_proj.weight"].T)
+            model._mlp(l, x)
+    last = x.view(b, -1, x.size(-1))[:, -1].contiguous()
     xf = ops.rmsnorm(last, model.weights["model.norm.weight"], c.rms_norm_eps)
     return torch.matmul(xf, model.lm_head.T)

@@ -147,3 +147,25 @@ def test_device_loop_matches_host_prepared_steps(dev):
     assert dev_tokens.tolist() == torch.stack(host_tokens).tolist()
     with pytest.raises(RuntimeError):
         runner.run_device_loop(k + 1)
+
+
+
+def test_chunked_prefill_matches_one_shot_and_oracle(dev):
+    """prefill_step with chunk_size: the same cache slots written with the
+    same K/V up to the projections' rounding (the library GEMM may pick
+    another kernel for the chunk's row count), last-token logits within the
+    oracle bars like the one-shot prefill's."""
+    b, s = 2, 70
+    model, cache, ref = build(dev, b, s, 2, tied=False)
+    ids = torch.randint(0, CFG["vocab_size"], (b, s), generator=torch.Generator().manual_seed(6))
+    seq = [0, 1]
+    cache.kv_cache.zero_()
+    one = prefill_step(model, ids.to(dev), seq)
+    kv_one = cache.kv_cache.clone()
+    cache.kv_cache.zero_()
+    chunked = prefill_step(model, ids.to(dev), seq, chunk_size=32)
+    assert torch.equal(cache.kv_cache != 0, kv_one != 0)
+    assert (cache.kv_cache.float() - kv_one.float()).abs().max().item() <= 2e-2
+    want = ref.prefill(ids, seq)
+    close(one, want)
+    close(chunked, want)
