@@ -210,7 +210,8 @@ MCE_API int mce_rope_kv_store(int dtype, void *query, void *query_out, void *key
  *   MCE_EPI_ADD    out += x w^T            (in-place residual add)
  *   MCE_EPI_SWIGLU w is [2n, k] (gate rows, then up rows);
  *                  out[:, j] = silu(x w_gate_j) * (x w_up_j)
- * x rows x_stride elements apart, out rows out_stride apart.  Needs
+ * x rows x_stride elements apart, out rows out_stride apart (out must not
+ * overlap x).  Needs
  * n % 16 == 0 and k in {2048, 3072, 4096}, or k == 8192 for m <= 8 without
  * SwiGLU; other shapes return MCE_ERR_UNSUPPORTED (callers then use a library
  * GEMM).

@@ -257,6 +257,14 @@ int decode_gemm_impl(const char *name, int dtype, const void *x, const void *nor
   MCE_REQUIRE(aligned16(x) && aligned16(w) && (!norm || aligned16(norm_w)) &&
                   (reinterpret_cast<uintptr_t>(out) & 7) == 0,
               "%s: x, w and the norm weight must be 16-byte aligned, out 8-byte aligned", name);
+  {
+    // every workgroup reads all of x while others already write their
+    // columns of out: the two must not overlap
+    const uintptr_t x0 = reinterpret_cast<uintptr_t>(x), o0 = reinterpret_cast<uintptr_t>(out);
+    const uintptr_t x1 = x0 + (uintptr_t)(((int64_t)(m - 1) * x_stride + k) * 2);
+    const uintptr_t o1 = o0 + (uintptr_t)(((int64_t)(m - 1) * out_stride + n) * 2);
+    MCE_REQUIRE(x1 <= o0 || o1 <= x0, "%s: out must not overlap x", name);
+  }
   MCE_REQUIRE((int64_t)n * k * (epilogue == MCE_EPI_SWIGLU ? 2 : 1) < ((int64_t)1 << 31),
               "%s: weight too large", name);
   DecodeGemmArgs a{};

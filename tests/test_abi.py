@@ -142,6 +142,10 @@ def test_decode_gemm_validation(lib):
     assert f(0, None, None, None, 9, 64, 8192, 8192, 64, 1, None) == _lib.MCE_ERR_UNSUPPORTED
     assert f(1, None, None, None, 8, 64, 2048, 2048, 64, 0, None) == _lib.MCE_ERR_UNSUPPORTED
     assert f(0, None, None, None, 0, 64, 2048, 2048, 64, 0, None) == _lib.MCE_OK
+    # out overlapping x (a residual add into the input itself) is refused
+    p = ctypes.c_void_p(1 << 20)
+    assert f(0, p, p, p, 8, 2048, 2048, 2048, 2048, 1, None) == _lib.MCE_ERR_INVALID
+    assert "overlap" in _err(lib)
 
 
 def test_rmsnorm_decode_gemm_validation(lib):
