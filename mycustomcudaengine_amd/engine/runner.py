@@ -160,6 +160,9 @@ class CUDAGraphRunner:
             raise RuntimeError(f"graph captured for {self.device_steps} device steps, got {steps}")
         cache = self.model.cache_manager
         for s, c in zip(self._seq_ids, self._ctx):
+            if c + steps - 1 > self.max_blocks_per_seq * cache.block_size:
+                raise RuntimeError(f"sequence {s} reaches position {c + steps - 2}, past the "
+                                   "block-table width captured in the graph")
             if c + steps - 1 > len(cache.block_tables[s]) * cache.block_size:
                 raise RuntimeError(f"sequence {s} has no block for position {c + steps - 2}")
         self.step_counter.zero_()
