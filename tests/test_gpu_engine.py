@@ -169,3 +169,56 @@ def test_chunked_prefill_matches_one_shot_and_oracle(dev):
     want = ref.prefill(ids, seq)
     close(one, want)
     close(chunked, want)
+
+
+def test_local_checkpoint_decode_step(dev, tmp_path):
+    """The reference's real-checkpoint test (tests/test_real_model_forward.py:
+    10-58: WeightLoader -> Llama3BConfig(loader.config) -> model, one decode
+    step of two sequences at position 0 through runner._prepare_inputs, no
+    NaN) on a synthetic local checkpoint in the Hugging Face layout: bf16
+    tensors over three sorted shards with an index file, tied embeddings (no
+    lm_head.weight), non-unit RMSNorm weights.  The logits are also checked
+    against the fp32 oracle on the weights as loaded (bf16 -> fp16)."""
+    import json
+    from safetensors.torch import save_file
+    from mycustomcudaengine_amd.engine.weight_loader import WeightLoader
+    w = random_llama_weights(CFG, seed=11, tied=True)
+    g = torch.Generator().manual_seed(12)
+    for k in w:
+        if k.endswith("norm.weight"):
+            w[k] = (1 + 0.1 * torch.randn(w[k].shape, generator=g)).half()
+    names = sorted(w)
+    parts = [names[i::3] for i in range(3)]
+    index = {"metadata": {}, "weight_map": {}}
+    for i, part in enumerate(parts):
+        fname = f"model-{i + 1:05d}-of-00003.safetensors"
+        save_file({k: w[k].to(torch.bfloat16).contiguous() for k in part}, str(tmp_path / fname))
+        index["weight_map"].update({k: fname for k in part})
+    (tmp_path / "model.safetensors.index.json").write_text(json.dumps(index))
+    (tmp_path / "config.json").write_text(json.dumps(dict(
+        CFG, architectures=["LlamaForCausalLM"], model_type="llama", torch_dtype="bfloat16",
+        tie_word_embeddings=True, bos_token_id=1)))
+
+    loader = WeightLoader(str(tmp_path), device=str(dev))
+    weights = loader.load_weights()
+    assert "lm_head.weight" not in weights and len(weights) == len(w)
+    assert all(t.dtype == torch.float16 and t.device == dev for t in weights.values())
+    config = Llama3BConfig(loader.config)
+    cache = KVCacheManager(num_blocks=200, block_size=16, num_layers=config.num_hidden_layers,
+                           num_heads=config.num_key_value_heads, head_dim=config.head_dim,
+                           dtype=torch.float16, device=dev)
+    model = Llama3BEngineModel(config, weights, cache)
+    runner = CUDAGraphRunner(model, max_batch_size=2)
+    ids = torch.tensor([[1], [1]], dtype=torch.int64, device=dev)
+    positions = torch.zeros((2, 1), dtype=torch.int32, device=dev)
+    context_lens = torch.ones(2, dtype=torch.int32, device=dev)
+    cache.allocate_sequence(0, 1)
+    cache.allocate_sequence(1, 1)
+    slot_mapping, block_tables, max_blocks = runner._prepare_inputs([0, 1], context_lens)
+    logits = model.decode_step(ids, positions, context_lens, slot_mapping, block_tables,
+                               max_blocks)
+    assert not torch.isnan(logits).any()
+    ref = LlamaRef(CFG, {k: v.to(torch.bfloat16).half() for k, v in w.items()})
+    close(logits, ref.decode(ids.cpu(), [0, 0], [0, 1]))
+    # both sequences saw the same token at the same position
+    assert torch.equal(logits[0], logits[1])
