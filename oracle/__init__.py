@@ -27,6 +27,8 @@ How each function is pinned (tests/test_oracle.py):
   decode_advance_ref     the allocator's slot_of() on the positions it yields,
                          -1 past the table width (hand-built cases).
   argmax_rows_ref        numpy.argmax; torch.argmax on ties and NaN rows.
+  prefill_paged_ref      the last S rows of prefill_attention_ref over the
+                         whole sequence (cached prefix + chunk).
   llama_*_ref            composition of the above with fp32 GEMMs; checked
                          against a torch-only decomposition of one layer.
 """
