@@ -296,13 +296,27 @@ MCE_API int mce_prefill_attention(int dtype, const void *query, const void *key,
  * prefill (benchmarks/benchmark_engine.py:64-89 with
  * csrc/kernels/prefill_attention.cu:271-309: contiguous K/V of the whole
  * prompt) to prompts processed in chunks against the cached prefix.
+ * Key split (optional): on small grids (batch * num_kv_heads *
+ * ceil(seq_len * G / 128) at most half the CUs: short chunks of few
+ * sequences) a non-null workspace of mce_prefill_attention_paged_workspace_size()
+ * bytes, 256-byte aligned (MCE_ERR_WORKSPACE otherwise; no initialisation;
+ * calls sharing one race), lets every query block whose keys span at least
+ * 1024 positions be cut into parts of at least 512 keys on separate
+ * workgroups, merged by a second launch.  It pays off behind long cached
+ * prefixes (the second launch costs a few microseconds even when no block is
+ * cut); with workspace == NULL, or on larger grids, the keys are not split.
  */
+/* Workspace bytes mce_prefill_attention_paged needs for this shape (0: none). */
+MCE_API size_t mce_prefill_attention_paged_workspace_size(int batch, int seq_len, int num_heads,
+                                                          int num_kv_heads);
+
 MCE_API int mce_prefill_attention_paged(int dtype, const void *query, const void *key_cache,
                                         const void *value_cache, const int32_t *block_tables,
                                         const int32_t *context_lens, void *output, int batch,
                                         int seq_len, int num_heads, int num_kv_heads,
                                         int head_dim, int max_blocks_per_seq, int block_size,
-                                        int64_t num_blocks, float scale, void *stream);
+                                        int64_t num_blocks, float scale, void *workspace,
+                                        size_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

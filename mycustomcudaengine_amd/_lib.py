@@ -53,9 +53,10 @@ SIGNATURES = {
     "mce_rmsnorm_decode_gemm": (_c_int, [_c_int, _vp, _vp, _c_f, _vp, _vp, _c_int, _c_int, _c_int,
                                          _c_i64, _c_i64, _c_int, _vp]),
     "mce_argmax_rows": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp]),
+    "mce_prefill_attention_paged_workspace_size": (_c_sz, [_c_int, _c_int, _c_int, _c_int]),
     "mce_prefill_attention_paged": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_int,
                                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
-                                             _c_i64, _c_f, _vp]),
+                                             _c_i64, _c_f, _vp, _c_sz, _vp]),
     "mce_decode_advance": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int,
                                     _c_int, _vp]),
     "mce_paged_attention_decode_rope": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

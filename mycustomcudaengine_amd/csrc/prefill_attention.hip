@@ -110,9 +110,36 @@ struct PrefillArgs {
   int maxb, bs_log2;
   int64_t num_blocks;
   uint32_t cache_bytes;  // bytes of one cache (< 2^31)
+  // key split across workgroups (paged mode, SPLITK): every item's key tiles
+  // are cut into nsplit parts, one workgroup each; part p of query row r
+  // leaves its unnormalised output ws_o[p][r][128] and (max, sum) ws_ml[p][r]
+  // (log2 units; max -inf for a part without keys of that row) for the merge.
+  int nsplit;
+  int64_t rows_all;  // B S Hq
+  float *ws_o, *ws_ml;
 };
 
 constexpr int PF_MAX_BLOCKS = 8192;  // paged mode: block-table row staged in LDS
+constexpr int PF_NRB_MERGE = 4;      // row blocks per item of the launches (PF_NRB)
+constexpr int PF_MAX_SPLIT = 8;      // key parts per item (SPLITK)
+// SPLITK: at least this many key tiles per part (a part's start-up, epilogue
+// and partial-state traffic cost about as much as streaming 8 to 16 tiles)
+constexpr int PF_MIN_PART_TILES = 16;
+
+// Keys of sequence b in the paged mode (its context length clamped into
+// [S, table capacity]).
+__device__ inline int paged_key_count(const PrefillArgs &a, int b) {
+  const int cap_keys = min(a.maxb << a.bs_log2, 1 << 30);
+  return min(max(a.context_lens[b], a.S), cap_keys);
+}
+// SPLITK: parts of query block `item` (rows item BM .. of one (sequence, kv
+// head)): its key tiles / PF_MIN_PART_TILES, at least 1 and at most nsplit.
+// One part means the workgroup of part 0 writes the output itself.
+__device__ inline int prefill_parts(const PrefillArgs &a, int key_S, int item, int BM) {
+  const int p0 = key_S - a.S;
+  const int n_ktiles = (p0 + min(a.S - 1, (item * BM + BM - 1) / a.G)) / PF_BN + 1;
+  return max(1, min(a.nsplit, n_ktiles / PF_MIN_PART_TILES));
+}
 
 // NRB row blocks of 32 rows per workgroup and KSPLIT key streams: wave w owns
 // row block w % NRB and key stream kh = w / NRB, which takes key tiles kh,
@@ -125,9 +152,13 @@ constexpr int PF_MAX_BLOCKS = 8192;  // paged mode: block-table row staged in LD
 // PAGED: K / V come from the page pool (chunked prefill: the queries are the
 // last S positions of each sequence and attend to all its cached keys); the
 // contiguous mode is PAGED = false with ctx_b = S.
-template <class T, int NRB, int KSPLIT, bool PAGED>
+// SPLITK (paged, two key streams): the workgroup takes part `part` of its
+// item's key tiles and writes that part's partial softmax state instead of
+// the output; prefill_merge_kernel combines the parts.
+template <class T, int NRB, int KSPLIT, bool PAGED, bool SPLITK>
 __global__ __launch_bounds__(NRB * KSPLIT * 64) __attribute__((amdgpu_waves_per_eu(PF_WAVES_PER_EU, PF_WAVES_PER_EU)))
 void prefill_causal_kernel(PrefillArgs a) {
+  static_assert(!SPLITK || (PAGED && KSPLIT == 2), "key parts: paged mode, two key streams");
   constexpr int BM = 32 * NRB;
   constexpr int NT = NRB * 64;                     // threads per key stream
   constexpr int K_PIECES = PF_BN * PF_HD / 8;      // 16-byte pieces per K tile
@@ -154,12 +185,18 @@ void prefill_causal_kernel(PrefillArgs a) {
   const int id = blockIdx.x;
   const int g = id % a.Hkv;
   const int b = (id / a.Hkv) % a.B;
-  const int item_rank = id / (a.Hkv * a.B);
+  const int rest = id / (a.Hkv * a.B);
+  const int part = SPLITK ? rest % a.nsplit : 0;
+  const int item_rank = SPLITK ? rest / a.nsplit : rest;
+  int tb = 0;  // first key tile of this workgroup's part (0 without SPLITK)
   const int G = a.G, S = a.S;
   // keys of this sequence and the position of its first query row
-  const int cap_keys = PAGED ? min(a.maxb << a.bs_log2, 1 << 30) : S;
-  const int key_S = PAGED ? min(max(a.context_lens[b], S), cap_keys) : S;
+  const int key_S = PAGED ? paged_key_count(a, b) : S;
   const int p0 = key_S - S;
+  // SPLITK: parts of this item (from its real key range); workgroups of
+  // parts past them have nothing to do
+  const int n_parts = SPLITK ? prefill_parts(a, key_S, a.n_items - 1 - item_rank, BM) : 1;
+  if (SPLITK && part >= n_parts) return;
   __shared__ int bt_lds[PAGED ? PF_MAX_BLOCKS : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -213,7 +250,7 @@ void prefill_causal_kernel(PrefillArgs a) {
   const int bsm = (1 << a.bs_log2) - 1;
   const int pkey = tid_h >> 4, pcol = (tid_h & 15) * 16;
   auto paged_off = [&](int u, int it) {
-    const int key = min((KSPLIT * u + kh) * PF_BN + pkey + it * (NT / 16), key_S - 1);
+    const int key = min((tb + KSPLIT * u + kh) * PF_BN + pkey + it * (NT / 16), key_S - 1);
     return bt_lds[key >> a.bs_log2] + (key & bsm) * kv_row * 2 + pcol;
   };
   // stream index u of this key stream <-> key tile KSPLIT u + kh
@@ -279,15 +316,21 @@ void prefill_causal_kernel(PrefillArgs a) {
   const int wave_min_pos = p0 + r_wave / G;
   const int item_max_pos = p0 + min(S - 1, (r_item + BM - 1) / G);
   const int n_ktiles = item_max_pos / PF_BN + 1;  // key tiles of the item
+  // SPLITK: this part's key tiles [tb, te)
+  if constexpr (SPLITK) tb = (int)((int64_t)part * n_ktiles / n_parts);
+  const int te = SPLITK ? (int)((int64_t)(part + 1) * n_ktiles / n_parts) : n_ktiles;
   // iterations per key stream, rounded up to even for the ping-pong unroll
-  const int n_iter = ((n_ktiles + KSPLIT - 1) / KSPLIT + 1) / 2 * 2;
+  const int n_iter = ((te - tb + KSPLIT - 1) / KSPLIT + 1) / 2 * 2;
   // key tiles this wave's rows need (none for a block of padding rows)
   const int n_wtiles =
       r_wave < rows_total ? (p0 + min(S - 1, min(r_wave + 31, rows_total - 1) / G)) / PF_BN + 1 : 0;
   // tiles [0, n_full) need no mask for this wave: every key <= its first
-  // position and < key_S
-  const int n_full = min((wave_min_pos + 1) / PF_BN, key_S / PF_BN);
-  const int lim = min(pos, key_S - 1) - 4 * hf;  // masked tiles: key offset limit + n0
+  // position and < key_S (SPLITK: and below the part's end, so that no key of
+  // the next part is ever scored into this part's state)
+  const int n_full = SPLITK ? min(min((wave_min_pos + 1) / PF_BN, key_S / PF_BN), te)
+                            : min((wave_min_pos + 1) / PF_BN, key_S / PF_BN);
+  // masked tiles: key offset limit + n0
+  const int lim = (SPLITK ? min(min(pos, key_S - 1), te * PF_BN - 1) : min(pos, key_S - 1)) - 4 * hf;
 
   // Q^T as MFMA B operand: lane supplies Q[pos, h][16 i + 8 hf + j], for fp16
   // pre-scaled by c (so the accumulators come out in log2 units); bf16 keeps
@@ -411,7 +454,7 @@ void prefill_causal_kernel(PrefillArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   {
     scores(ks_h, 0.f, s_a);
-    prep(s_a, kh);
+    prep(s_a, tb + kh);
     const float mx = rowmax(s_a);
     if (__ballot(mx > thr) != 0) rescale(mx, s_a);
   }
@@ -438,7 +481,7 @@ void prefill_causal_kernel(PrefillArgs a) {
   auto step = [&](const int u, const int set, floatx16 &s_cur, floatx16 &s_nxt, auto diag) {
     constexpr bool DIAG = decltype(diag)::value;
     lds_barrier();
-    const int kt = KSPLIT * u + kh;  // key tile
+    const int kt = tb + KSPLIT * u + kh;  // key tile
     const uint16_t *kp = &ks_h[((u + 1) & 1) * KS_SIZE + r32 * KS_PITCH + 8 * hf];
     // V^T fragment (dt, kk): lane l = 16 q + s of group q takes dims 32 dt +
     // 16 (q & 1) + 0..15 and keys 16 kk + 4 (q >> 1) + 0..3 (first read) and
@@ -504,7 +547,7 @@ void prefill_causal_kernel(PrefillArgs a) {
   };
   // step u needs the mask from u_first on (its next tile KSPLIT (u+1) + kh
   // reaches n_full); tile KSPLIT u + kh is past this wave's rows from u_end on
-  const int nf_rel = n_full - kh, nw_rel = n_wtiles - kh;
+  const int nf_rel = n_full - tb - kh, nw_rel = min(n_wtiles, te) - tb - kh;
   const int u_first = nf_rel <= KSPLIT ? 0 : (nf_rel + KSPLIT - 1) / KSPLIT - 1;
   const int u_end = nw_rel <= 0 ? 0 : (nw_rel + KSPLIT - 1) / KSPLIT;
   const int u1 = u_first & ~1;                      // <= u_end <= n_iter
@@ -560,11 +603,41 @@ void prefill_causal_kernel(PrefillArgs a) {
     // a state that never saw an unmasked key (m = -inf, l = 0, O = 0) gets
     // weight 0; stream 0 always sees key 0, so mm is finite on real rows
     const float mm = fmaxf(m_own, m_oth);
-    const float a_own = fast_exp2(m_own - mm), a_oth = fast_exp2(m_oth - mm);
-    const float inv = 1.0f / xor32_add(l_i * a_own + l_oth * a_oth);
+    // (a part may hold no key of a row in either stream: mm = -inf)
+    const float mmz = SPLITK && mm == -INFINITY ? 0.f : mm;
+    const float a_own = fast_exp2(m_own - mmz), a_oth = fast_exp2(m_oth - mmz);
+    const float l_row = xor32_add(l_i * a_own + l_oth * a_oth);
+    xr = reinterpret_cast<const floatx4 *>(xo) + (ko * NRB + rb) * 8 * 64 + lane;
+    if (SPLITK && n_parts > 1) {
+      // this part's state of the row: O unnormalised (dims OUT_DIMS kh ..),
+      // relative to max mm, and the row sum; straight from the MFMA layout
+      const int grow = r_wave + r32;
+      if (grow < rows_total) {
+        const int p = grow / G, hh = g * G + (grow - p * G);
+        const int64_t pr = (int64_t)part * a.rows_all + ((int64_t)b * S + p) * a.Hq + hh;
+        float *dst = a.ws_o + pr * PF_HD + OUT_DIMS * kh + 4 * hf;
+#pragma unroll
+        for (int dd = 0; dd < OUT_DIMS / 32; ++dd)
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4) {
+            const floatx4 x = xr[(dd * 4 + e4) * 64];
+            floatx4 v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int e = 4 * e4 + j;
+              v[j] = (kh == 0 ? o[dd][e] : o[2 + dd][e]) * a_own + x[j] * a_oth;
+            }
+            *reinterpret_cast<floatx4 *>(dst + 32 * dd + 8 * e4) = v;
+          }
+        if (kh == 0 && hf == 0)
+          *reinterpret_cast<float2 *>(a.ws_ml + pr * 2) =
+              float2{l_row > 0.f ? mm : -INFINITY, l_row};
+      }
+      return;
+    }
+    const float inv = 1.0f / l_row;
     s_own = a_own * inv;
     s_oth = a_oth * inv;
-    xr = reinterpret_cast<const floatx4 *>(xo) + (ko * NRB + rb) * 8 * 64 + lane;
   } else {
     s_own = 1.0f / xor32_add(l_i);
   }
@@ -608,6 +681,50 @@ void prefill_causal_kernel(PrefillArgs a) {
   }
 }
 
+// Merge of the key parts (SPLITK): one thread per (query row, dim), two rows
+// per 256-thread workgroup; rows of single-part items were written by the
+// attention kernel.  Every row has a part with keys (key 0 is in every row's
+// range), so the max M is finite and parts without keys weigh 0.
+template <class T>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
+  const int64_t row = (int64_t)blockIdx.x * 2 + (threadIdx.x >> 7);
+  const int d = threadIdx.x & 127;
+  if (row >= a.rows_all) return;
+  // row = (b S + qi) Hq + h; its query block: rows qi G + h % G of (b, h / G)
+  const int h = (int)(row % a.Hq);
+  const int64_t bq = row / a.Hq;
+  const int b = (int)(bq / a.S), qi = (int)(bq - (int64_t)b * a.S);
+  const int item = (qi * a.G + h % a.G) / (32 * PF_NRB_MERGE);
+  const int n_parts = prefill_parts(a, paged_key_count(a, b), item, 32 * PF_NRB_MERGE);
+  if (n_parts <= 1) return;
+  float m[PF_MAX_SPLIT], l[PF_MAX_SPLIT], o[PF_MAX_SPLIT];
+#pragma unroll
+  for (int p = 0; p < PF_MAX_SPLIT; ++p) {
+    if (p < n_parts) {
+      const int64_t pr = (int64_t)p * a.rows_all + row;
+      const float2 ml = *reinterpret_cast<const float2 *>(a.ws_ml + pr * 2);
+      m[p] = ml.x;
+      l[p] = ml.y;
+      o[p] = a.ws_o[pr * PF_HD + d];
+    } else {
+      m[p] = -INFINITY;
+      l[p] = 0.f;
+      o[p] = 0.f;
+    }
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int p = 0; p < PF_MAX_SPLIT; ++p) M = fmaxf(M, m[p]);
+  float L = 0.f, A = 0.f;
+#pragma unroll
+  for (int p = 0; p < PF_MAX_SPLIT; ++p) {
+    const float w = p < n_parts ? fast_exp2(m[p] - M) : 0.f;
+    L += w * l[p];
+    A += w * o[p];
+  }
+  a.out[row * PF_HD + d] = T::from_float(A / L);
+}
+
 }  // namespace mce
 
 using namespace mce;
@@ -619,25 +736,55 @@ namespace {
 // CUs that free up first (longest-processing-time-first scheduling).  The
 // key range is split over two wave sets when the grid alone would not give
 // every CU about two workgroups (long causal sequences, small batch).
-constexpr int PF_NRB = 4;
+constexpr int PF_NRB = PF_NRB_MERGE;
 
+int64_t prefill_items(int64_t S, int G) { return (S * G + 32 * PF_NRB - 1) / (32 * PF_NRB); }
+
+// Key parts per item of the paged mode: grids that leave more than half of
+// the CUs without a workgroup (few long sequences, a short chunk behind a
+// cached prefix) cut every item's keys into at most as many parts as keep all
+// workgroups in one wave of one per CU (a second round of workgroups costs
+// more than the longer parts); 1 = no split.
+int prefill_paged_parts(int batch, int seq_len, int num_heads, int num_kv_heads) {
+  if (batch <= 0 || seq_len <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return 1;
+  const int64_t grid = prefill_items(seq_len, num_heads / num_kv_heads) * batch * num_kv_heads;
+  if (2 * grid > (int64_t)cu_count()) return 1;
+  const int64_t n = (int64_t)cu_count() / grid;
+  return (int)(n > PF_MAX_SPLIT ? PF_MAX_SPLIT : n);
+}
+
+// a.nsplit > 1: key parts (paged mode), partials in a.ws_o / a.ws_ml, then
+// the merge launch
 template <bool PAGED>
 int prefill_launch(int dtype, PrefillArgs &a, void *stream, const char *name) {
-  a.n_items = (int)(((int64_t)a.S * a.G + 32 * PF_NRB - 1) / (32 * PF_NRB));
-  const int64_t grid = (int64_t)a.n_items * a.B * a.Hkv;
+  a.n_items = (int)prefill_items(a.S, a.G);
+  const int64_t grid = (int64_t)a.n_items * a.B * a.Hkv * (a.nsplit > 1 ? a.nsplit : 1);
   MCE_REQUIRE(grid < ((int64_t)1 << 31), "%s: problem too large", name);
   hipStream_t st = (hipStream_t)stream;
-  const bool split = grid < 2 * (int64_t)cu_count();
+  const bool two_streams = grid < 2 * (int64_t)cu_count();
+  if constexpr (PAGED) {
+    if (a.nsplit > 1) {
+      const unsigned mgrid = (unsigned)((a.rows_all + 1) / 2);
+      if (dtype == MCE_F16) {
+        prefill_causal_kernel<F16T, PF_NRB, 2, true, true><<<(unsigned)grid, PF_NRB * 128, 0, st>>>(a);
+        prefill_merge_kernel<F16T><<<mgrid, 256, 0, st>>>(a);
+      } else {
+        prefill_causal_kernel<BF16T, PF_NRB, 2, true, true><<<(unsigned)grid, PF_NRB * 128, 0, st>>>(a);
+        prefill_merge_kernel<BF16T><<<mgrid, 256, 0, st>>>(a);
+      }
+      return check_launch(name);
+    }
+  }
   if (dtype == MCE_F16) {
-    if (split)
-      prefill_causal_kernel<F16T, PF_NRB, 2, PAGED><<<(unsigned)grid, PF_NRB * 128, 0, st>>>(a);
+    if (two_streams)
+      prefill_causal_kernel<F16T, PF_NRB, 2, PAGED, false><<<(unsigned)grid, PF_NRB * 128, 0, st>>>(a);
     else
-      prefill_causal_kernel<F16T, PF_NRB, 1, PAGED><<<(unsigned)grid, PF_NRB * 64, 0, st>>>(a);
+      prefill_causal_kernel<F16T, PF_NRB, 1, PAGED, false><<<(unsigned)grid, PF_NRB * 64, 0, st>>>(a);
   } else {
-    if (split)
-      prefill_causal_kernel<BF16T, PF_NRB, 2, PAGED><<<(unsigned)grid, PF_NRB * 128, 0, st>>>(a);
+    if (two_streams)
+      prefill_causal_kernel<BF16T, PF_NRB, 2, PAGED, false><<<(unsigned)grid, PF_NRB * 128, 0, st>>>(a);
     else
-      prefill_causal_kernel<BF16T, PF_NRB, 1, PAGED><<<(unsigned)grid, PF_NRB * 64, 0, st>>>(a);
+      prefill_causal_kernel<BF16T, PF_NRB, 1, PAGED, false><<<(unsigned)grid, PF_NRB * 64, 0, st>>>(a);
   }
   return check_launch(name);
 }
@@ -684,12 +831,21 @@ extern "C" int mce_prefill_attention(int dtype, const void *query,
   return prefill_launch<false>(dtype, a, stream, "mce_prefill_attention");
 }
 
+extern "C" size_t mce_prefill_attention_paged_workspace_size(int batch, int seq_len,
+                                                          int num_heads, int num_kv_heads) {
+  const int parts = prefill_paged_parts(batch, seq_len, num_heads, num_kv_heads);
+  if (parts <= 1) return 0;
+  const size_t rows = (size_t)batch * seq_len * num_heads * parts;
+  return ((rows * PF_HD * sizeof(float) + 255) & ~(size_t)255) + rows * 2 * sizeof(float);
+}
+
 extern "C" int mce_prefill_attention_paged(int dtype, const void *query, const void *key_cache,
                                            const void *value_cache, const int32_t *block_tables,
                                            const int32_t *context_lens, void *output, int batch,
                                            int seq_len, int num_heads, int num_kv_heads,
                                            int head_dim, int max_blocks_per_seq, int block_size,
-                                           int64_t num_blocks, float scale, void *stream) {
+                                           int64_t num_blocks, float scale, void *workspace,
+                                           size_t workspace_bytes, void *stream) {
   clear_error();
   const char *name = "mce_prefill_attention_paged";
   MCE_REQUIRE(dtype == MCE_F16 || dtype == MCE_BF16, "%s: unknown dtype %d", name, dtype);
@@ -736,5 +892,19 @@ extern "C" int mce_prefill_attention_paged(int dtype, const void *query, const v
   a.bs_log2 = ilog2(block_size);
   a.num_blocks = num_blocks;
   a.cache_bytes = (uint32_t)cache_bytes;
+  // the key split runs only when the caller hands in a workspace
+  a.nsplit = workspace ? prefill_paged_parts(batch, seq_len, num_heads, num_kv_heads) : 1;
+  if (a.nsplit > 1) {
+    const size_t need = mce_prefill_attention_paged_workspace_size(batch, seq_len, num_heads,
+                                                                   num_kv_heads);
+    if (workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255) != 0)
+      return set_error(MCE_ERR_WORKSPACE,
+                       "%s: a 256-byte aligned workspace of %zu bytes is required (%zu given)",
+                       name, need, workspace_bytes);
+    a.rows_all = (int64_t)batch * seq_len * num_heads;
+    a.ws_o = (float *)workspace;
+    a.ws_ml = (float *)((char *)workspace +
+                        (((size_t)a.rows_all * a.nsplit * PF_HD * sizeof(float) + 255) & ~(size_t)255));
+  }
   return prefill_launch<true>(dtype, a, stream, name);
 }

@@ -89,8 +89,9 @@ def _prefill_chunked(model, input_ids: torch.Tensor, seq_ids: List[int],
             rope_kv_store(q.view(b * n, hq, d), k.view(b * n, hkv, d), v.view(b * n, hkv, d),
                           kv[l, 0], kv[l, 1], model.cos_table, model.sin_table,
                           positions.view(-1), slots)
+            # keys split over workgroups only behind a long cached prefix
             attn = prefill_attention_paged(q.view(b, n, hq, d), kv[l, 0], kv[l, 1], tables, ctx,
-                                           model.scale)
+                                           model.scale, split_keys=c0 >= 1024)
             x.addmm_(attn.view(b * n, hq * d), model.weights[f"{p}.self_attn.o_proj.weight"].T)
             model._mlp(l, x)
     last = x.view(b, -1, x.size(-1))[:, -1].contiguous()

@@ -513,7 +513,8 @@ def prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tenso
 
 def prefill_attention_paged(query: torch.Tensor, key_cache: torch.Tensor,
                             value_cache: torch.Tensor, block_tables: torch.Tensor,
-                            context_lens: torch.Tensor, scale: float) -> torch.Tensor:
+                            context_lens: torch.Tensor, scale: float,
+                            split_keys: bool = True) -> torch.Tensor:
     """Chunked causal prefill attention reading K/V from the page pool.
 
     query [B, S, Hq, D] holds the last S positions of each sequence; sequence
@@ -523,7 +524,13 @@ def prefill_attention_paged(query: torch.Tensor, key_cache: torch.Tensor,
     position context_lens[b] - S + i and attends to keys 0 .. that position.
     Returns [B, S, Hq, D].  Widens the reference's prefill
     (benchmarks/benchmark_engine.py:64-89, contiguous K/V of the whole prompt)
-    to prompts processed in chunks against the cached prefix."""
+    to prompts processed in chunks against the cached prefix.
+
+    split_keys: on small grids (few sequences, short chunks) let query blocks
+    with long key ranges (a cached prefix of about 1024 tokens or more) split
+    their keys over several workgroups, merged by a second launch that costs a
+    few microseconds even when nothing is split; pass False when the prefixes
+    are known to be short."""
     dev = _on_gpu("prefill_attention_paged", query, key_cache, value_cache, block_tables,
                   context_lens)
     code = _dtype_code(query, "prefill_attention_paged query")
@@ -545,8 +552,15 @@ def prefill_attention_paged(query: torch.Tensor, key_cache: torch.Tensor,
     q = query if query.is_contiguous() else query.contiguous()
     out = torch.empty_like(q)
     with _on_device(dev):
+        lib = _lib.load()
+        # small grids split each query block's keys over workgroups (partials
+        # in a workspace, merged by a second launch)
+        ws_bytes = (lib.mce_prefill_attention_paged_workspace_size(b, s, hq, hkv)
+                    if split_keys and b and s else 0)
+        ws = torch.empty(ws_bytes + 256, dtype=torch.uint8, device=dev) if ws_bytes else None
+        ws_ptr = (ws.data_ptr() + 255) & ~255 if ws is not None else None
         _lib.call("mce_prefill_attention_paged", code, q.data_ptr(), key_cache.data_ptr(),
                   value_cache.data_ptr(), block_tables.data_ptr(), context_lens.data_ptr(),
                   out.data_ptr(), b, s, hq, hkv, d, block_tables.size(1), bs, nb, float(scale),
-                  _stream(dev))
+                  ws_ptr, ws_bytes, _stream(dev))
     return out

@@ -17,7 +17,7 @@ HEADER_ENTRY_POINTS = {
     "mce_paged_attention_decode", "mce_rope_inplace", "mce_prefill_attention",
     "mce_rope_kv_store", "mce_decode_gemm", "mce_paged_attention_decode_rope",
     "mce_rmsnorm_decode_gemm", "mce_argmax_rows", "mce_decode_advance",
-    "mce_prefill_attention_paged",
+    "mce_prefill_attention_paged", "mce_prefill_attention_paged_workspace_size",
 }
 
 
@@ -207,7 +207,7 @@ def test_decode_loop_entry_points_validate(lib):
 def test_prefill_paged_validation(lib):
     f = lib.mce_prefill_attention_paged
     one = ctypes.c_void_p(16)  # non-null, never dereferenced: validation fails first
-    args = [0, one, one, one, one, one, one, 2, 64, 24, 8, 128, 8, 16, 64, 0.1, None]
+    args = [0, one, one, one, one, one, one, 2, 64, 24, 8, 128, 8, 16, 64, 0.1, None, 0, None]
     # (args itself is valid and would launch: only invalid variants are called)
     bad = list(args); bad[11] = 64
     assert f(*bad) == _lib.MCE_ERR_INVALID and "head_dim" in _err(lib)
@@ -223,3 +223,16 @@ def test_prefill_paged_validation(lib):
     assert f(*bad) == _lib.MCE_ERR_INVALID and "2 GiB" in _err(lib)
     empty = list(args); empty[8] = 0
     assert f(*empty) == _lib.MCE_OK
+    # one sequence, a 64-query chunk: 2 items x 8 kv heads = 16 workgroups, so
+    # a workspace given for the key split must be large enough and aligned
+    # (no GPU: 256 CUs assumed)
+    ws = lib.mce_prefill_attention_paged_workspace_size
+    need = ws(1, 64, 24, 8)
+    assert need >= 8 * 64 * 24 * 130 * 4
+    split = list(args); split[7] = 1
+    split[17] = need - 1; split[16] = ctypes.c_void_p(1 << 20)
+    assert f(*split) == _lib.MCE_ERR_WORKSPACE and "workspace" in _err(lib)
+    split[17] = need; split[16] = ctypes.c_void_p((1 << 20) + 16)   # misaligned
+    assert f(*split) == _lib.MCE_ERR_WORKSPACE
+    # grids of at least half the CUs need none
+    assert ws(8, 512, 24, 8) == 0 and ws(0, 64, 24, 8) == 0 and ws(1, 2048, 24, 8) == 0

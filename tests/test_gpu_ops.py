@@ -508,29 +508,43 @@ def _paged_case(seed, prefixes, s, dtype=torch.float16, hq=24, hkv=8, bs=16):
     return q, kc, vc, table, torch.tensor(ctx, dtype=torch.int32)
 
 
+# Grids of at most 128 workgroups (B x Hkv x ceil(3 s / 128), on a 256-CU
+# MI355X) take the key-split kernel, which cuts a query block's keys into
+# parts of at least 16 tiles (512 keys) merged by a second launch: the prefix
+# 2000 / 3584 / 1500 cases run 4, 5 and 3 parts (the 700-token sequence next
+# to the 1500 one stays whole), the other small grids one part (the output
+# written by the attention kernel); the last two cases are larger grids.
 @pytest.mark.parametrize("prefixes,s,dtype", [([0, 37], 64, torch.float16),
                                               ([100, 5, 300], 17, torch.float16),
                                               ([700], 1, torch.float16),
                                               ([129], 300, torch.float16),
                                               ([2000], 48, torch.float16),
-                                              ([0, 64], 96, torch.bfloat16)])
+                                              ([0, 64], 96, torch.bfloat16),
+                                              ([3584], 512, torch.float16),
+                                              ([1500, 700], 64, torch.bfloat16),
+                                              ([0, 37, 500], 300, torch.float16),
+                                              ([1000, 0, 3000, 17], 200, torch.bfloat16)])
 def test_prefill_paged_matches_oracle(dev, prefixes, s, dtype):
     from mycustomcudaengine_amd.ops import prefill_attention_paged
     q, kc, vc, table, ctx = _paged_case(160 + s + len(prefixes), prefixes, s, dtype)
     scale = 1.0 / 128 ** 0.5
-    out = prefill_attention_paged(q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), ctx.to(dev),
-                                  scale).cpu()
-    assert not torch.isnan(out).any()
-    for i in range(len(prefixes)):
-        ref = prefill_paged_ref(q[i], kc, vc, table[i].tolist(), int(ctx[i]), scale)
-        err = (out[i].float() - ref).abs().max().item()
-        assert err <= TOL, (i, err)
+    args = (q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), ctx.to(dev), scale)
+    refs = [prefill_paged_ref(q[i], kc, vc, table[i].tolist(), int(ctx[i]), scale)
+            for i in range(len(prefixes))]
+    for split in (True, False):  # with and without the key split of small grids
+        out = prefill_attention_paged(*args, split_keys=split).cpu()
+        assert not torch.isnan(out).any()
+        for i, ref in enumerate(refs):
+            err = (out[i].float() - ref).abs().max().item()
+            assert err <= TOL, (split, i, err)
 
 
-@pytest.mark.parametrize("b,s", [(1, 2048), (2, 333), (8, 512)])
+@pytest.mark.parametrize("b,s", [(1, 2048), (3, 333), (8, 512), (1, 300), (2, 64)])
 def test_prefill_paged_without_prefix_equals_contiguous(dev, b, s):
     """No cached prefix (context == chunk): the paged kernel gives exactly the
-    bits of mce_prefill_attention on the same K/V laid out contiguously."""
+    bits of mce_prefill_attention on the same K/V laid out contiguously, also
+    from the key-split kernel of small grids (the last two cases: one part
+    per query block, so the same arithmetic in the same order)."""
     from mycustomcudaengine_amd.ops import prefill_attention_paged
     q, kc, vc, table, ctx = _paged_case(170 + b, [0] * b, s)
     k = torch.stack([gather_kv_rows(kc, table[i], s) for i in range(b)])
