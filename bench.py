@@ -16,8 +16,12 @@ Extra fields on the same JSON line:
             decode steps replayed via hipGraph: tok/s, ms/step, TTFT.
   cpu_baseline  the CPU oracle on the same cfg2 inputs, on this host's cores.
 
+  chunked   (--only chunked; not in the default run) chunked prefill from the
+            page pool, B=1 chunk 512 behind 0-7680 cached tokens and B=4 chunk
+            128 behind 2048, with and without the key split: us, TFLOP/s.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--only decode|prefill|splitk]
+                       [--only decode|prefill|splitk|model|chunked]
 (--only runs one workload; only the default run prints the full result line.)
 """
 from __future__ import annotations
@@ -124,6 +128,39 @@ def bench_prefill(case, dev, steps, warmup):
     graph_ms = time_graph(fn, steps, warmup)
     flops = case.algorithmic_flops()
     return ms, flops, flops / (ms * 1e-3) / 1e12, graph_ms
+
+
+def bench_chunked(dev, steps: int, warmup: int) -> dict:
+    """Chunked prefill attention from the page pool (ops.prefill_attention_paged):
+    synthetic fp16 Q/K/V ~ N(0, 1), 24/8 heads, 16-token pages in a shuffled
+    pool, every sequence's chunk behind `prefix` cached tokens; timed with the
+    key split allowed (split_keys=True) and not.  Algorithmic FLOPs: QK^T and
+    PV over the causal pairs, 4 * D * Hq * sum_i (prefix + i + 1) per sequence."""
+    from mycustomcudaengine_amd.ops import prefill_attention_paged
+    g = torch.Generator(device=dev).manual_seed(47)
+    out = {}
+    for b, prefix, s in ((1, 0, 512), (1, 1536, 512), (1, 3584, 512), (1, 7680, 512),
+                         (4, 2048, 128)):
+        ctx, bs, hq, hkv, d = prefix + s, 16, 24, 8, 128
+        width = (ctx + bs - 1) // bs
+        nb = b * width
+        kc = torch.randn(nb, bs, hkv, d, generator=g, device=dev).half()
+        vc = torch.randn(nb, bs, hkv, d, generator=g, device=dev).half()
+        table = torch.randperm(nb, generator=g, device=dev).view(b, width).to(torch.int32)
+        q = torch.randn(b, s, hq, d, generator=g, device=dev).half()
+        cl = torch.full((b,), ctx, dtype=torch.int32, device=dev)
+        flops = 4 * d * hq * b * sum(prefix + i + 1 for i in range(s))
+        row = {}
+        for split in (True, False):
+            ms = time_gpu(lambda: prefill_attention_paged(q, kc, vc, table, cl, d ** -0.5,
+                                                          split_keys=split), steps, warmup)
+            row["split" if split else "whole"] = {"us": round(ms * 1e3, 2),
+                                                  "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+        key = f"B{b}_prefix{prefix}_chunk{s}"
+        out[key] = row
+        log(f"chunked {key}: key split {row['split']['us']} us, whole {row['whole']['us']} us")
+        del kc, vc, q
+    return out
 
 
 def bench_model(dev, steps: int = 128, batch: int = 8, prompt: int = 512, seed: int = 46) -> dict:
@@ -268,7 +305,8 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "prefill", "splitk", "model"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "splitk", "model", "chunked"],
+                    default=None)
     ap.add_argument("--calibration-copy", action="store_true",
                     help="first copy 256 MiB device-to-device (a kernel of known traffic, "
                          "used to scale rocprofv3 FETCH_SIZE/WRITE_SIZE readings)")
@@ -335,6 +373,9 @@ def main() -> None:
         log(f"cfg5 model: {extra['model']['tok_s']} tok/s, {extra['model']['ms_per_step']} ms/step "
             f"(host-prepared steps: {extra['model']['tok_s_host_prepared']} tok/s)")
         torch.cuda.empty_cache()
+
+    if args.only == "chunked":
+        extra["chunked"] = bench_chunked(dev, max(20, args.steps // 4), 5)
 
     if "decode" not in result:  # a single non-headline workload was asked for
         print(json.dumps({"metric": METRIC, "only": args.only, **extra}), flush=True)

@@ -681,48 +681,57 @@ void prefill_causal_kernel(PrefillArgs a) {
   }
 }
 
-// Merge of the key parts (SPLITK): one thread per (query row, dim), two rows
-// per 256-thread workgroup; rows of single-part items were written by the
-// attention kernel.  Every row has a part with keys (key 0 is in every row's
-// range), so the max M is finite and parts without keys weigh 0.
+// Merge of the key parts (SPLITK): 32 threads per query row (4 dims each), 8
+// rows per 256-thread workgroup; rows of single-part items were written by
+// the attention kernel.  The context length and every slot's (max, sum) and O
+// are loaded together (one memory round trip); slots past the row's part
+// count hold another call's data and are dropped by selects.  Every row has a
+// part with keys (key 0 is in every row's range), so the max M is finite and
+// parts without keys weigh 0.
 template <class T>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
-  const int64_t row = (int64_t)blockIdx.x * 2 + (threadIdx.x >> 7);
-  const int d = threadIdx.x & 127;
+  const int64_t row = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+  const int d4 = (threadIdx.x & 31) * 4;
   if (row >= a.rows_all) return;
   // row = (b S + qi) Hq + h; its query block: rows qi G + h % G of (b, h / G)
   const int h = (int)(row % a.Hq);
   const int64_t bq = row / a.Hq;
   const int b = (int)(bq / a.S), qi = (int)(bq - (int64_t)b * a.S);
   const int item = (qi * a.G + h % a.G) / (32 * PF_NRB_MERGE);
-  const int n_parts = prefill_parts(a, paged_key_count(a, b), item, 32 * PF_NRB_MERGE);
-  if (n_parts <= 1) return;
-  float m[PF_MAX_SPLIT], l[PF_MAX_SPLIT], o[PF_MAX_SPLIT];
+  const int key_S = paged_key_count(a, b);
+  float2 ml[PF_MAX_SPLIT];
+  floatx4 o[PF_MAX_SPLIT];
 #pragma unroll
   for (int p = 0; p < PF_MAX_SPLIT; ++p) {
-    if (p < n_parts) {
+    if (p < a.nsplit) {
       const int64_t pr = (int64_t)p * a.rows_all + row;
-      const float2 ml = *reinterpret_cast<const float2 *>(a.ws_ml + pr * 2);
-      m[p] = ml.x;
-      l[p] = ml.y;
-      o[p] = a.ws_o[pr * PF_HD + d];
+      ml[p] = *reinterpret_cast<const float2 *>(a.ws_ml + pr * 2);
+      o[p] = *reinterpret_cast<const floatx4 *>(a.ws_o + pr * PF_HD + d4);
     } else {
-      m[p] = -INFINITY;
-      l[p] = 0.f;
-      o[p] = 0.f;
+      ml[p] = float2{-INFINITY, 0.f};
+      o[p] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
   }
+  const int n_parts = prefill_parts(a, key_S, item, 32 * PF_NRB_MERGE);
+  if (n_parts <= 1) return;
   float M = -INFINITY;
 #pragma unroll
-  for (int p = 0; p < PF_MAX_SPLIT; ++p) M = fmaxf(M, m[p]);
-  float L = 0.f, A = 0.f;
+  for (int p = 0; p < PF_MAX_SPLIT; ++p)
+    if (p < n_parts) M = fmaxf(M, ml[p].x);
+  float L = 0.f;
+  floatx4 A = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int p = 0; p < PF_MAX_SPLIT; ++p) {
-    const float w = p < n_parts ? fast_exp2(m[p] - M) : 0.f;
-    L += w * l[p];
-    A += w * o[p];
+    const float w = fast_exp2(ml[p].x - M);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) A[j] = p < n_parts ? A[j] + w * o[p][j] : A[j];
+    L = p < n_parts ? L + w * ml[p].y : L;
   }
-  a.out[row * PF_HD + d] = T::from_float(A / L);
+  const float inv = 1.0f / L;
+  u32x2 v;
+  v[0] = pack2<T>(A[0] * inv, A[1] * inv);
+  v[1] = pack2<T>(A[2] * inv, A[3] * inv);
+  *reinterpret_cast<u32x2 *>(a.out + row * PF_HD + d4) = v;
 }
 
 }  // namespace mce
@@ -764,7 +773,7 @@ int prefill_launch(int dtype, PrefillArgs &a, void *stream, const char *name) {
   const bool two_streams = grid < 2 * (int64_t)cu_count();
   if constexpr (PAGED) {
     if (a.nsplit > 1) {
-      const unsigned mgrid = (unsigned)((a.rows_all + 1) / 2);
+      const unsigned mgrid = (unsigned)((a.rows_all + 7) / 8);
       if (dtype == MCE_F16) {
         prefill_causal_kernel<F16T, PF_NRB, 2, true, true><<<(unsigned)grid, PF_NRB * 128, 0, st>>>(a);
         prefill_merge_kernel<F16T><<<mgrid, 256, 0, st>>>(a);
