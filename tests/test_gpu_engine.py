@@ -171,6 +171,18 @@ def test_chunked_prefill_matches_one_shot_and_oracle(dev):
     close(chunked, want)
 
 
+def test_chunked_prefill_behind_long_prefix_splits_keys(dev):
+    """A 1300-token prompt in 512-position chunks: the third chunk runs behind
+    a 1024-token cached prefix, where prefill_step asks for the key split
+    (one sequence: a 96-workgroup grid, so its query blocks' keys are cut in
+    two parts and merged); logits within the oracle bars."""
+    b, s = 1, 1300
+    model, cache, ref = build(dev, b, s, 2, tied=False)
+    ids = torch.randint(0, CFG["vocab_size"], (b, s), generator=torch.Generator().manual_seed(8))
+    chunked = prefill_step(model, ids.to(dev), [0], chunk_size=512)
+    close(chunked, ref.prefill(ids, [0]))
+
+
 def test_local_checkpoint_decode_step(dev, tmp_path):
     """The reference's real-checkpoint test (tests/test_real_model_forward.py:
     10-58: WeightLoader -> Llama3BConfig(loader.config) -> model, one decode
