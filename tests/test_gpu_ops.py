@@ -559,3 +559,31 @@ def test_prefill_paged_without_prefix_equals_contiguous(dev, b, s):
 def gather_kv_rows(cache, row, n):
     from oracle.ops_ref import gather_kv
     return gather_kv(cache, row.tolist(), n)
+
+
+def test_prefill_paged_key_split_graph_replays(dev):
+    """The key split (attention + merge launches, torch-allocated workspace)
+    captured in a HIP graph and replayed several times, with an eager call
+    of another shape in between: every replay equals the eager result bit
+    for bit."""
+    from mycustomcudaengine_amd.ops import prefill_attention_paged
+    q, kc, vc, table, ctx = (t.to(dev) for t in _paged_case(180, [2000], 48))
+    other = [t.to(dev) for t in _paged_case(181, [1500, 700], 64)]
+    scale = 1.0 / 128 ** 0.5
+    eager = prefill_attention_paged(q, kc, vc, table, ctx, scale)
+    s_ = torch.cuda.Stream(device=dev)
+    s_.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(s_):
+        prefill_attention_paged(q, kc, vc, table, ctx, scale)
+    torch.cuda.current_stream(dev).wait_stream(s_)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = prefill_attention_paged(q, kc, vc, table, ctx, scale)
+    other_eager = prefill_attention_paged(*other, scale)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+        again = prefill_attention_paged(*other, scale)
+        torch.cuda.synchronize()
+        assert torch.equal(again.view(torch.int16), other_eager.view(torch.int16))
