@@ -1,0 +1,120 @@
+"""GPU: seeded random sweeps over the attention kernels' valid shapes, each
+against the CPU oracle (max-abs 1e-2 of fp32, no NaN from the NaN-filled
+unused pool pages).
+
+Decode: batch 1-40, 1-16 kv heads (several head groups above 8), GQA group
+1-8, block sizes 8-256, contexts 0 to several thousand (per-sequence and
+split-K modes, empty sequences), fp16 and bf16.  Prefill: contiguous batch
+1-3, 1-900 positions, 1-8 kv heads, group 1-8; chunked from the page pool
+with prefixes up to 2500 tokens, pages of 16-64 tokens, with and without the
+key split.
+"""
+import math
+import random
+
+import pytest
+import torch
+
+import my_cuda_engine_cpp as ops
+from mycustomcudaengine_amd.ops import prefill_attention_paged
+from oracle.inputs import make_decode_case, make_prefill_case
+from oracle.ops_ref import decode_attention_ref, prefill_attention_ref, prefill_paged_ref
+
+TOL = 1e-2
+pytestmark = pytest.mark.gpu
+
+
+def _decode_config(i):
+    r = random.Random(1000 + i)
+    b = r.randint(1, 40)
+    hkv = r.choice([1, 2, 4, 8, 16])
+    g = r.randint(1, 8)
+    bs = r.choice([8, 16, 32, 64, 128, 256])
+    dtype = r.choice([torch.float16, torch.bfloat16])
+    top = max(2, min(6000, 1_000_000 // (b * hkv)))
+    ctx = [r.choice([0, 1, r.randint(1, 64), r.randint(1, top), r.randint(top // 2, top)])
+           for _ in range(b)]
+    extra = r.randint(0, 3)
+    return b, hkv, g, bs, dtype, ctx, extra
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_decode_sweep(dev, i):
+    b, hkv, g, bs, dtype, ctx, extra = _decode_config(i)
+    need = max(1, max((c + bs - 1) // bs for c in ctx))
+    case = make_decode_case(2000 + i, b, ctx, num_heads=hkv * g, num_kv_heads=hkv, block_size=bs,
+                            max_blocks=need + extra, dtype=dtype)
+    desc = f"B={b} hkv={hkv} G={g} bs={bs} {dtype} max_ctx={max(ctx)} width={need + extra}"
+    print(desc, flush=True)
+    out = ops.paged_attention_decode(
+        case.query.to(dev), case.key_cache.to(dev), case.value_cache.to(dev),
+        case.block_tables.to(dev), case.context_lens.to(dev), case.max_blocks,
+        case.block_size, case.scale).cpu()
+    ref = decode_attention_ref(case.query, case.key_cache, case.value_cache,
+                               case.block_tables, case.context_lens, case.scale)
+    assert not torch.isnan(out).any(), desc
+    err = (out.float() - ref).abs().max().item()
+    assert err <= TOL, (desc, err)
+
+
+@pytest.mark.parametrize("i", range(8))
+def test_prefill_sweep(dev, i):
+    r = random.Random(3000 + i)
+    b, s = r.randint(1, 3), r.choice([1, r.randint(2, 64), r.randint(65, 900)])
+    hkv, g = r.choice([1, 2, 8]), r.randint(1, 8)
+    dtype = r.choice([torch.float16, torch.bfloat16])
+    desc = f"B={b} S={s} hkv={hkv} G={g} {dtype}"
+    print(desc, flush=True)
+    case = make_prefill_case(4000 + i, b, s, num_heads=hkv * g, num_kv_heads=hkv, dtype=dtype)
+    out = ops.prefill_attention(case.query.to(dev), case.key.to(dev), case.value.to(dev),
+                                case.scale).cpu()
+    ref = prefill_attention_ref(case.query, case.key, case.value, case.scale)
+    assert not torch.isnan(out).any(), desc
+    err = (out.float() - ref).abs().max().item()
+    assert err <= TOL, (desc, err)
+
+
+def _pool_case(r, prefixes, s, hq, hkv, bs, dtype):
+    """Shuffled page pool, unused pages NaN; sequence i holds prefixes[i] + s
+    tokens."""
+    g = torch.Generator().manual_seed(r.randint(0, 1 << 30))
+    b = len(prefixes)
+    ctx = [p + s for p in prefixes]
+    width = max((c + bs - 1) // bs for c in ctx) + r.randint(0, 2)
+    nb = b * width + 3
+    kc = torch.full((nb, bs, hkv, 128), float("nan"), dtype=dtype)
+    vc = torch.full((nb, bs, hkv, 128), float("nan"), dtype=dtype)
+    perm = torch.randperm(nb, generator=g)
+    table = torch.zeros(b, width, dtype=torch.int32)
+    for i in range(b):
+        blocks = perm[i * width:(i + 1) * width]
+        table[i] = blocks.to(torch.int32)
+        used = (ctx[i] + bs - 1) // bs
+        kc[blocks[:used]] = torch.randn(used, bs, hkv, 128, generator=g).to(dtype)
+        vc[blocks[:used]] = torch.randn(used, bs, hkv, 128, generator=g).to(dtype)
+    q = torch.randn(b, s, hq, 128, generator=g).to(dtype)
+    return q, kc, vc, table, torch.tensor(ctx, dtype=torch.int32)
+
+
+@pytest.mark.parametrize("i", range(8))
+def test_prefill_paged_sweep(dev, i):
+    r = random.Random(5000 + i)
+    b = r.randint(1, 3)
+    prefixes = [r.choice([0, r.randint(1, 300), r.randint(1000, 2500)]) for _ in range(b)]
+    s = r.choice([1, r.randint(2, 100), r.randint(100, 600)])
+    hkv, g = r.choice([2, 8]), r.randint(1, 4)
+    bs = r.choice([16, 32, 64])
+    dtype = r.choice([torch.float16, torch.bfloat16])
+    desc = f"prefixes={prefixes} S={s} hkv={hkv} G={g} bs={bs} {dtype}"
+    print(desc, flush=True)
+    q, kc, vc, table, ctx = _pool_case(r, prefixes, s, hkv * g, hkv, bs, dtype)
+    scale = 1.0 / math.sqrt(128)
+    refs = [prefill_paged_ref(q[j], kc, vc, table[j].tolist(), int(ctx[j]), scale)
+            for j in range(b)]
+    args = (q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), ctx.to(dev), scale)
+    for split in (True, False):
+        out = prefill_attention_paged(*args, split_keys=split).cpu()
+        assert not torch.isnan(out).any(), (desc, split)
+        for j, ref in enumerate(refs):
+            err = (out[j].float() - ref).abs().max().item()
+            assert err <= TOL, (desc, split, j, err)
