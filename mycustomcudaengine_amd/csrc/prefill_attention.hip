@@ -7,13 +7,14 @@
 // and every K/V tile staged in LDS serves all of them (the reference stages
 // K/V once per query head).
 //
-// Work items: a workgroup takes BM = 32 * NW consecutive rows of one (b, g).
+// Work items: a workgroup takes BM = 32 * NRB consecutive rows of one (b, g).
 // Causal cost grows with the row index, so workgroups are numbered heaviest
-// item first.
+// item first.  Small grids run two key streams per item (even / odd key
+// tiles, 8 waves) merged through LDS at the end.
 //
 // Each wave owns 32 rows and uses v_mfma_f32_32x32x16_f16 throughout:
-//   S^T[64 keys x 32 rows] = K . Q^T   (A = K from LDS, B = Q^T in registers)
-//     -> lane l holds the scores of row (l % 32) for 32 of the 64 keys, so the
+//   S^T[32 keys x 32 rows] = K . Q^T   (A = K from LDS, B = Q^T in registers)
+//     -> lane l holds the scores of row (l % 32) for 16 of the 32 keys, so the
 //        row softmax is in-lane plus one exchange with lane l ^ 32.
 //   O^T[128 dims x 32 rows] += V^T . P^T (A = V^T from LDS, B = P^T straight
 //     from the S^T registers, converted to f16): lane l again holds row
@@ -30,7 +31,7 @@
 // straight-line block as the softmax and P V of tile k, so the exp/convert
 // VALU work of one tile runs while the matrix cores work on the other.  K and
 // V^T are double-buffered in LDS (K one tile ahead of V) with one barrier per
-// tile; the next tiles are fetched into registers a full tile ahead.
+// tile; tiles are fetched into registers two tiles ahead of their staging.
 //
 // Softmax in the log2 domain: Q is pre-scaled by c = scale log2(e) when it is
 // loaded, and each score accumulator starts at -m (the row's running max, in
@@ -39,6 +40,13 @@
 // row's max grows by more than 2^8 in p units, so most tiles skip it and p
 // stays below 256, well inside fp16.  Row sums are taken with v_dot2 over the
 // same f16 P values that enter P V.
+//
+// Paged mode (chunked prefill): K / V rows come from the page pool through
+// the block table (page byte offsets staged in LDS), the queries being each
+// sequence's last S positions.  Its key split (small grids behind long cached
+// prefixes) gives every query block up to nsplit workgroups over disjoint key
+// ranges, each leaving an unnormalised partial state that
+// prefill_merge_kernel combines by log-sum-exp.
 #include "mce_common.h"
 
 #include <type_traits>
