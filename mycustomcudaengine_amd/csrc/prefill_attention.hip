@@ -120,8 +120,11 @@ struct PrefillArgs {
   uint32_t cache_bytes;  // bytes of one cache (< 2^31)
   // key split across workgroups (paged mode, SPLITK): every item's key tiles
   // are cut into nsplit parts, one workgroup each; part p of query row r
-  // leaves its unnormalised output ws_o[p][r][128] and (max, sum) ws_ml[p][r]
-  // (log2 units; max -inf for a part without keys of that row) for the merge.
+  // leaves its output ws_o[p][r][128] and (max, sum) ws_ml[p][r] (log2
+  // units; max -inf for a part without keys of that row) for the merge.  The
+  // fp16 kernels store that output normalised by the part's sum, in fp16
+  // (half the bytes); the bf16 kernels store it unnormalised in fp32 (a bf16
+  // copy would round too coarsely).
   int nsplit;
   int64_t rows_all;  // B S Hq
   float *ws_o, *ws_ml;
@@ -623,7 +626,9 @@ void prefill_causal_kernel(PrefillArgs a) {
       if (grow < rows_total) {
         const int p = grow / G, hh = g * G + (grow - p * G);
         const int64_t pr = (int64_t)part * a.rows_all + ((int64_t)b * S + p) * a.Hq + hh;
-        float *dst = a.ws_o + pr * PF_HD + OUT_DIMS * kh + 4 * hf;
+        const int64_t off = pr * PF_HD + OUT_DIMS * kh + 4 * hf;
+        constexpr bool NORM_F16 = T::code == MCE_F16;
+        const float sc = NORM_F16 ? (l_row > 0.f ? 1.0f / l_row : 0.f) : 1.0f;
 #pragma unroll
         for (int dd = 0; dd < OUT_DIMS / 32; ++dd)
 #pragma unroll
@@ -633,9 +638,17 @@ void prefill_causal_kernel(PrefillArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const int e = 4 * e4 + j;
-              v[j] = (kh == 0 ? o[dd][e] : o[2 + dd][e]) * a_own + x[j] * a_oth;
+              v[j] = ((kh == 0 ? o[dd][e] : o[2 + dd][e]) * a_own + x[j] * a_oth) * sc;
             }
-            *reinterpret_cast<floatx4 *>(dst + 32 * dd + 8 * e4) = v;
+            if constexpr (NORM_F16) {
+              u32x2 h;
+              h[0] = pack2<T>(v[0], v[1]);
+              h[1] = pack2<T>(v[2], v[3]);
+              *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(a.ws_o) + off + 32 * dd +
+                                         8 * e4) = h;
+            } else {
+              *reinterpret_cast<floatx4 *>(a.ws_o + off + 32 * dd + 8 * e4) = v;
+            }
           }
         if (kh == 0 && hf == 0)
           *reinterpret_cast<float2 *>(a.ws_ml + pr * 2) =
@@ -714,7 +727,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
     if (p < a.nsplit) {
       const int64_t pr = (int64_t)p * a.rows_all + row;
       ml[p] = *reinterpret_cast<const float2 *>(a.ws_ml + pr * 2);
-      o[p] = *reinterpret_cast<const floatx4 *>(a.ws_o + pr * PF_HD + d4);
+      if constexpr (T::code == MCE_F16) {  // normalised fp16 partials
+        const u32x2 h = *reinterpret_cast<const u32x2 *>(
+            reinterpret_cast<const uint16_t *>(a.ws_o) + pr * PF_HD + d4);
+        o[p] = floatx4{T::lo(h[0]), T::hi(h[0]), T::lo(h[1]), T::hi(h[1])};
+      } else {
+        o[p] = *reinterpret_cast<const floatx4 *>(a.ws_o + pr * PF_HD + d4);
+      }
     } else {
       ml[p] = float2{-INFINITY, 0.f};
       o[p] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -731,8 +750,10 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
 #pragma unroll
   for (int p = 0; p < PF_MAX_SPLIT; ++p) {
     const float w = fast_exp2(ml[p].x - M);
+    // normalised fp16 partials carry their sum separately
+    const float wo = T::code == MCE_F16 ? w * ml[p].y : w;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) A[j] = p < n_parts ? A[j] + w * o[p][j] : A[j];
+    for (int j = 0; j < 4; ++j) A[j] = p < n_parts ? A[j] + wo * o[p][j] : A[j];
     L = p < n_parts ? L + w * ml[p].y : L;
   }
   const float inv = 1.0f / L;
