@@ -14,7 +14,9 @@ Extra fields on the same JSON line:
   splitk    cfg4 long-context decode (B=8, ctx 32768): GB/s.
   model     cfg5 Llama-3.2-3B random-init, B=8, prefill 512 then 128 greedy
             decode steps replayed via hipGraph: tok/s, ms/step, TTFT.
-  cpu_baseline  the CPU oracle on the same cfg2 inputs, on this host's cores.
+  cpu_baseline  the CPU oracle on the same cfg2 inputs, on this host's cores
+            (prefill and splitk carry their own, on cfg3 / cfg4; cfg5 has none:
+            an fp32 CPU forward of the 3B model is not a bounded sample).
 
   chunked   (--only chunked; not in the default run) chunked prefill from the
             page pool, B=1 chunk 512 behind 0-7680 cached tokens and B=4 chunk
@@ -288,6 +290,44 @@ def cpu_baseline_decode(case) -> dict:
                       f"{med * 1e3:.1f} ms/run; {info['cpu_model']}; torch {info['torch']}"}
 
 
+def cpu_median_s(fn, runs: int = 3, warmup: int = 1) -> tuple:
+    """Median wall seconds of `runs` calls of a CPU oracle function (after
+    `warmup` calls), on all of this host's cores."""
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def cpu_baseline_prefill(case) -> dict:
+    """cfg3 on the CPU: the fp32 causal-attention oracle on the same inputs."""
+    from oracle.ops_ref import prefill_attention_ref
+    med, n = cpu_median_s(lambda: prefill_attention_ref(case.query, case.key, case.value,
+                                                        case.scale))
+    return {"value": round(case.algorithmic_flops() / med / 1e12, 4), "unit": "TFLOP/s",
+            "cores": len(os.sched_getaffinity(0)), "kind": "port",
+            "sample": f"full cfg3 (B=1, S=2048), fp32 torch oracle, median of {n} runs after "
+                      f"1 warmup, {med * 1e3:.1f} ms/run"}
+
+
+def cpu_baseline_splitk(case) -> dict:
+    """cfg4 on the CPU: the fp32 decode-attention oracle on the same inputs."""
+    from oracle.ops_ref import decode_attention_ref
+    med, n = cpu_median_s(lambda: decode_attention_ref(
+        case.query, case.key_cache, case.value_cache, case.block_tables, case.context_lens,
+        case.scale))
+    return {"value": round(case.algorithmic_bytes() / med / 1e9, 3), "unit": "GB/s",
+            "cores": len(os.sched_getaffinity(0)), "kind": "port",
+            "sample": f"full cfg4 (B=8, ctx 32768), fp32 torch oracle, median of {n} runs after "
+                      f"1 warmup, {med * 1e3:.1f} ms/run"}
+
+
 def measured_traffic():
     """HBM bytes per decode-kernel launch from the committed rocprofv3
     FETCH_SIZE/WRITE_SIZE passes (calibrated against a 256 MiB copy), or None
@@ -355,6 +395,9 @@ def main() -> None:
                             "frac_of_fp16_dense_peak": round(tfs / FP16_DENSE_TFLOPS, 4),
                             "timing": "back-to-back eager calls, HIP events",
                             "graph_replay_us": round(pgms * 1e3, 2)}
+        if not args.no_cpu:
+            extra["prefill"]["cpu_baseline"] = cpu_baseline_prefill(case3)
+            log(f"cfg3 CPU baseline: {extra['prefill']['cpu_baseline']['value']} TFLOP/s")
         del case3
     if args.only in (None, "splitk"):
         log("generating cfg4 inputs")
@@ -364,6 +407,9 @@ def main() -> None:
         extra["splitk"] = {"workload": "cfg4 paged decode B=8 ctx=32768 24/8 heads D=128",
                            "us": round(kms * 1e3, 2), "bytes": kbytes,
                            "gbs": round(kgbs, 1), "frac_of_hbm_peak": round(kgbs / HBM_PEAK_GBS, 4)}
+        if not args.no_cpu:
+            extra["splitk"]["cpu_baseline"] = cpu_baseline_splitk(case4)
+            log(f"cfg4 CPU baseline: {extra['splitk']['cpu_baseline']['value']} GB/s")
         del case4
         torch.cuda.empty_cache()
 
