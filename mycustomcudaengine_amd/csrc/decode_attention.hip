@@ -77,10 +77,11 @@ struct DecodeArgs {
   const int32_t *btab;      // [B, maxb]
   const int32_t *ctx_lens;  // [B]
   uint16_t *out;            // [B, Hq, HD]
-  float *ws_ml;             // [B, Hq, J, 2]
-  float *ws_acc;            // [B, Hq, J, HD]
+  float *ws_ml;             // [B, Hq, P, 2]
+  float *ws_acc;            // [B, Hq, P, HD]
   int *ws_nparts;           // [B] workgroups covering each sequence
   int B, Hq, Hkv, maxb, bs_log2, J;
+  int P;                    // part slots per row: min(J, table tiles) (a part holds >= 1 tile)
   int hpg, wph;             // kv heads per workgroup, waves per kv head
   int per_seq;              // 1: workgroup (group, b) covers all of sequence b
   int64_t q_stride_b;       // elements between the query rows of two sequences
@@ -570,7 +571,7 @@ void paged_decode_kernel(DecodeArgs a) {
               o[k] = pack2<T>(acc[h][2 * k] * inv, acc[h][2 * k + 1] * inv);
             *reinterpret_cast<u32x4 *>(a.out + (row0 + h) * HD + lr * 8) = o;
           } else {
-            const int64_t pr = (row0 + h) * a.J + slot;
+            const int64_t pr = (row0 + h) * a.P + slot;
             float *dst = a.ws_acc + pr * HD + lr * 8;
             *reinterpret_cast<floatx4 *>(dst) =
                 floatx4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
@@ -620,7 +621,7 @@ void paged_decode_kernel(DecodeArgs a) {
       if (nparts == 1) {
         a.out[row * HD + d] = T::from_float(A / L);
       } else {
-        const int64_t pr = row * a.J + slot;
+        const int64_t pr = row * a.P + slot;
         a.ws_acc[pr * HD + d] = A;
         if (d == 0) {
           a.ws_ml[pr * 2] = M;
@@ -640,18 +641,18 @@ template <class T>
 __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int64_t row = (int64_t)b * a.Hq + h;
-  const float *ml = a.ws_ml + row * a.J * 2;
-  const float *ac = a.ws_acc + row * a.J * HD + d;
+  const float *ml = a.ws_ml + row * a.P * 2;
+  const float *ac = a.ws_acc + row * a.P * HD + d;
   // The part count, the first HD parts' (m, l) and this lane's dim of the
   // first SPEC parts' partial outputs are loaded together (one memory round
   // trip); slots at or past the count are never used (the workspace holds
-  // J >= parts slots per row, so these reads stay inside it).
+  // P >= parts slots per row, so these reads stay inside it).
   constexpr int SPEC = 16;
   const int n_raw = a.ws_nparts[b];
-  const float2 ml0 = d < a.J ? *reinterpret_cast<const float2 *>(ml + 2 * d) : float2{0.f, 0.f};
+  const float2 ml0 = d < a.P ? *reinterpret_cast<const float2 *>(ml + 2 * d) : float2{0.f, 0.f};
   float v0[SPEC];
 #pragma unroll
-  for (int k = 0; k < SPEC; ++k) v0[k] = k < a.J ? ac[(int64_t)k * HD] : 0.f;
+  for (int k = 0; k < SPEC; ++k) v0[k] = k < a.P ? ac[(int64_t)k * HD] : 0.f;
   const int n = __builtin_amdgcn_readfirstlane(n_raw);
   if (n <= 1) return;
   __shared__ float w_lds[HD], wl_lds[HD], mx_lds[2];
@@ -710,19 +711,24 @@ __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
 }
 
 struct DecodeLayout {
-  int J, hpg, wph, groups;
+  int J, P, hpg, wph, groups;
   size_t ml_off, acc_off, nparts_off, total;
 };
 
-static DecodeLayout decode_layout(int batch, int num_heads, int num_kv_heads) {
+// P: part slots per (sequence, query head) row.  Every workgroup range holds
+// at least one tile, so a sequence of T tiles has at most T parts, and T is
+// at most the table capacity in tiles.
+static DecodeLayout decode_layout(int batch, int num_heads, int num_kv_heads, int64_t cap_tokens) {
   DecodeLayout L{};
   L.hpg = num_kv_heads < DEC_NW ? num_kv_heads : DEC_NW;
   L.wph = DEC_NW / L.hpg;
   L.groups = (num_kv_heads + L.hpg - 1) / L.hpg;
   int J = cu_count() / L.groups;
   L.J = J < 1 ? 1 : (J > 512 ? 512 : J);
+  const int64_t cap_tiles = (cap_tokens + TILE - 1) / TILE;
+  L.P = (int)(cap_tiles < L.J ? (cap_tiles < 1 ? 1 : cap_tiles) : L.J);
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  const size_t rows = (size_t)batch * num_heads * L.J;
+  const size_t rows = (size_t)batch * num_heads * L.P;
   L.ml_off = 0;
   L.acc_off = up(rows * 2 * sizeof(float));
   L.nparts_off = up(L.acc_off + rows * HD * sizeof(float));
@@ -742,7 +748,8 @@ extern "C" size_t mce_paged_attention_decode_workspace_size(
     return 0;
   // short contexts run the per-sequence mode, which needs no workspace
   if ((int64_t)max_blocks_per_seq * block_size <= PER_SEQ_MAX_TOKENS) return 0;
-  return decode_layout(batch, num_heads, num_kv_heads).total;
+  return decode_layout(batch, num_heads, num_kv_heads,
+                       (int64_t)max_blocks_per_seq * block_size).total;
 }
 
 namespace {
@@ -793,7 +800,8 @@ int decode_impl(int dtype, const void *query, const void *key_cache, const void 
   MCE_REQUIRE((int64_t)batch * ((int64_t)max_blocks_per_seq * block_size / TILE + 1) <
                   ((int64_t)1 << 30),
               "mce_paged_attention_decode: batch x context too large");
-  const DecodeLayout Lay = decode_layout(batch, num_heads, num_kv_heads);
+  const DecodeLayout Lay = decode_layout(batch, num_heads, num_kv_heads,
+                                         (int64_t)max_blocks_per_seq * block_size);
   const bool per_seq = (int64_t)max_blocks_per_seq * block_size <= PER_SEQ_MAX_TOKENS;
   if (!per_seq && (workspace == nullptr || workspace_bytes < Lay.total ||
                    (reinterpret_cast<uintptr_t>(workspace) & 255) != 0))
@@ -828,6 +836,7 @@ int decode_impl(int dtype, const void *query, const void *key_cache, const void 
   a.maxb = max_blocks_per_seq;
   a.bs_log2 = ilog2(block_size);
   a.J = Lay.J;
+  a.P = Lay.P;
   a.hpg = Lay.hpg;
   a.wph = Lay.wph;
   // Short contexts: one workgroup per (kv head, sequence) streams the whole
