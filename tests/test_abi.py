@@ -103,6 +103,18 @@ def test_decode_workspace_size(lib):
     assert 0 < small < big
     assert big % 256 == 0
 
+    # rows of P = min(J, table tiles) part slots: (m, l) and 128 partial dims in
+    # fp32, then the per-sequence part counts; J = 256 workgroups (no GPU: 256
+    # CUs assumed, one group of 8 kv heads)
+    def expect(b, hq, cap_tokens):
+        up = lambda x: (x + 255) // 256 * 256
+        p = min(256, (cap_tokens + 31) // 32)
+        rows = b * hq * p
+        return up(rows * 2 * 4) + up(rows * 128 * 4) + up(b * 4)
+    assert big == expect(32, 24, 256 * 16)          # cfg2: 128 slots
+    assert f(8, 24, 8, 2048, 16) == expect(8, 24, 2048 * 16)   # cfg4: J = 256 slots
+    assert f(32, 24, 8, 100, 16) == expect(32, 24, 1600)       # 50 slots
+
 
 def test_rope_and_prefill_validation(lib):
     assert lib.mce_rope_inplace(0, None, None, None, None, None, 1, 1, 2, 1, 7, 16,
