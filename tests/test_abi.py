@@ -5,6 +5,7 @@ No test here launches a kernel: every call below fails validation (or is a
 pure size query), so it runs on a machine without a GPU.
 """
 import ctypes
+import os
 
 import pytest
 import torch
@@ -248,3 +249,18 @@ def test_prefill_paged_validation(lib):
     assert f(*split) == _lib.MCE_ERR_WORKSPACE
     # grids of at least half the CUs need none
     assert ws(8, 512, 24, 8) == 0 and ws(0, 64, 24, 8) == 0 and ws(1, 2048, 24, 8) == 0
+
+
+def test_header_compiles_as_c_and_cpp(tmp_path):
+    """include/mce_abi.h is usable from plain C (cgo / JNI / FFI hosts) and C++."""
+    import shutil
+    import subprocess
+    inc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+    for comp, std, ext in (("gcc", "-std=c99", "c"), ("g++", "-std=c++17", "cpp")):
+        if shutil.which(comp) is None:
+            pytest.skip(f"{comp} not available")
+        src = tmp_path / f"use.{ext}"
+        src.write_text('#include "mce_abi.h"\nint main(void) { return mce_abi_version() > 0 ? 0 : 1; }\n')
+        r = subprocess.run([comp, std, "-Wall", "-Wextra", "-Werror", "-fsyntax-only", "-I", inc,
+                            str(src)], capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
