@@ -165,6 +165,12 @@ class CUDAGraphRunner:
                                    "block-table width captured in the graph")
             if c + steps - 1 > len(cache.block_tables[s]) * cache.block_size:
                 raise RuntimeError(f"sequence {s} has no block for position {c + steps - 2}")
+        # The replays read static_block_tables, which the last capture_graph /
+        # execute filled; blocks appended since (append_token) are copied in
+        # here, or decode_advance would map their positions to block 0.
+        b = len(self._seq_ids)
+        self.static_block_tables[:b].copy_(
+            torch.from_numpy(cache.block_table_array(self._seq_ids, self.max_blocks_per_seq)))
         self.step_counter.zero_()
         for _ in range(steps):
             self.cuda_graph.replay()

@@ -29,6 +29,17 @@ How each function is pinned (tests/test_oracle.py):
   argmax_rows_ref        numpy.argmax; torch.argmax on ties and NaN rows.
   prefill_paged_ref      the last S rows of prefill_attention_ref over the
                          whole sequence (cached prefix + chunk).
-  llama_*_ref            composition of the above with fp32 GEMMs; checked
-                         against a torch-only decomposition of one layer.
+  LlamaRef (model_ref)   tests/test_model_oracle.py: with every projection
+                         weight zero the layers are the identity, so logits
+                         equal rms_norm(embed[ids]) @ embed^T; an independent
+                         forward built from library routines (F.rms_norm,
+                         causal SDPA with enable_gqa, F.silu, complex-
+                         exponential RoPE) on non-unit norm weights, for
+                         prefill and prefill + decode; each of nine planted
+                         mistakes in that forward (a dropped residual, gate
+                         and up swapped, RoPE on v or missing on k, norms
+                         swapped or unweighted, a wrong GQA map, no causal
+                         mask, a shifted position) must move the logits far
+                         outside the tolerance.  Also prefill(S) ==
+                         prefill(S - 1) + decode (tests/test_engine_cpu.py).
 """

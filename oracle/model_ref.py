@@ -91,25 +91,34 @@ class LlamaRef:
 
 
 def random_llama_weights(cfg: dict, seed: int, device="cpu", std: float = 0.02,
-                         tied: bool = True) -> dict:
-    """Random-init Llama weights ~ N(0, std) (RMSNorm weights = 1), keyed by
-    the Hugging Face names; lm_head tied to the embedding unless tied=False."""
+                         tied: bool = True, norm_std: float = 0.0) -> dict:
+    """Random-init Llama weights ~ N(0, std), keyed by the Hugging Face names;
+    lm_head tied to the embedding unless tied=False.  RMSNorm weights are 1
+    (as in every reference harness, benchmarks/benchmark_engine.py:180-181)
+    unless norm_std > 0: then 1 + N(0, norm_std), drawn from a second
+    generator so the other tensors keep the values a given seed gives them."""
     g = torch.Generator().manual_seed(seed)
+    gn = torch.Generator().manual_seed(seed + 1_000_003)
     hid, inter = cfg["hidden_size"], cfg["intermediate_size"]
     hq, hkv, d = cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"]
 
     def rnd(*shape):
         return (torch.randn(*shape, generator=g) * std).to(torch.float16).to(device)
 
+    def norm():
+        w = torch.ones(hid)
+        if norm_std > 0:
+            w = w + torch.randn(hid, generator=gn) * norm_std
+        return w.to(torch.float16).to(device)
+
     w = {"model.embed_tokens.weight": rnd(cfg["vocab_size"], hid),
-         "model.norm.weight": torch.ones(hid, dtype=torch.float16, device=device)}
+         "model.norm.weight": norm()}
     if not tied:
         w["lm_head.weight"] = rnd(cfg["vocab_size"], hid)
     for l in range(cfg["num_hidden_layers"]):
         p = f"model.layers.{l}"
-        w[f"{p}.input_layernorm.weight"] = torch.ones(hid, dtype=torch.float16, device=device)
-        w[f"{p}.post_attention_layernorm.weight"] = torch.ones(hid, dtype=torch.float16,
-                                                              device=device)
+        w[f"{p}.input_layernorm.weight"] = norm()
+        w[f"{p}.post_attention_layernorm.weight"] = norm()
         w[f"{p}.self_attn.q_proj.weight"] = rnd(hq * d, hid)
         w[f"{p}.self_attn.k_proj.weight"] = rnd(hkv * d, hid)
         w[f"{p}.self_attn.v_proj.weight"] = rnd(hkv * d, hid)

@@ -84,3 +84,17 @@ def test_model_oracle_prefill_equals_prefill_plus_decode():
     ref.prefill(ids[:, :6], [0, 1])
     step = ref.decode(ids[:, 6:7], [6, 6], [0, 1])
     assert torch.allclose(full, step, atol=1e-5)
+
+
+def test_reference_engine_import_path():
+    """The reference's callers import engine.cache, engine.runner,
+    engine.weight_loader and engine.models.llama (benchmarks/
+    benchmark_engine.py:7-9, engine/runner.py:5); those paths resolve to this
+    engine's classes."""
+    import mycustomcudaengine_amd.engine as mine
+    from engine.cache import KVCacheManager as A
+    from engine.models.llama import Llama3BConfig as B, Llama3BEngineModel as C
+    from engine.runner import CUDAGraphRunner as D
+    from engine.weight_loader import WeightLoader as E
+    assert (A, B, C, D, E) == (mine.KVCacheManager, mine.Llama3BConfig, mine.Llama3BEngineModel,
+                               mine.CUDAGraphRunner, mine.WeightLoader)

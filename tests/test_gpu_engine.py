@@ -23,7 +23,8 @@ CFG = dict(hidden_size=3072, intermediate_size=8192, num_hidden_layers=2,
 
 
 def build(dev, batch, prompt, gen, seed=5, tied=True):
-    w_cpu = random_llama_weights(CFG, seed=seed, tied=tied)
+    # non-unit RMSNorm weights, so a swapped or dropped norm weight shows
+    w_cpu = random_llama_weights(CFG, seed=seed, tied=tied, norm_std=0.1)
     weights = {k: v.to(dev) for k, v in w_cpu.items()}
     cache = KVCacheManager(num_blocks=batch * ((prompt + gen + 15) // 16) + 8, block_size=16,
                            num_layers=CFG["num_hidden_layers"], num_heads=8, head_dim=128,
@@ -148,6 +149,36 @@ def test_device_loop_matches_host_prepared_steps(dev):
     with pytest.raises(RuntimeError):
         runner.run_device_loop(k + 1)
 
+
+
+def test_device_loop_sees_blocks_appended_after_capture(dev):
+    """The graph is captured with a block table wider than the blocks the
+    sequences own; blocks appended afterwards (append_token) must reach the
+    replayed steps: run_device_loop copies the allocator's tables into the
+    graph's table first (otherwise the new positions would map to block 0,
+    another sequence's page).  Tokens equal the host-prepared steps'."""
+    b, s, k = 2, 30, 6
+    model, cache, _ = build(dev, b, s, 1)  # each sequence owns blocks for 31 tokens
+    seq = [0, 1]
+    ids = torch.randint(0, CFG["vocab_size"], (b, s), generator=torch.Generator().manual_seed(9))
+    logits = prefill_step(model, ids.to(dev), seq)
+    tok0 = logits.argmax(-1, keepdim=True)
+    runner = CUDAGraphRunner(model, max_batch_size=b)
+    runner.capture_graph(tok0, torch.full((b, 1), s, dtype=torch.int32, device=dev), seq,
+                         [s + 1] * b, max_blocks=4, device_steps=k)
+    assert all(len(cache.block_tables[q]) == 2 for q in seq)
+    for q in seq:  # positions 32.. need a third block
+        cache.append_token(q, 32)
+    dev_tokens = runner.run_device_loop(k).cpu()
+    tok = tok0
+    host_tokens = []
+    for i in range(k):
+        p = s + i
+        out = runner.execute(tok, torch.full((b, 1), p, dtype=torch.int32, device=dev), seq,
+                             [p + 1] * b)
+        tok = out.argmax(-1, keepdim=True)
+        host_tokens.append(tok.view(-1).cpu())
+    assert dev_tokens.tolist() == torch.stack(host_tokens).tolist()
 
 
 def test_chunked_prefill_matches_one_shot_and_oracle(dev):
