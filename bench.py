@@ -10,25 +10,32 @@ too and reported beside it).
 
 Extra fields on the same JSON line:
   prefill   cfg3 causal prefill (S=2048, 24/8 heads): algorithmic TFLOP/s
-            (2 * D * Hq * S * (S+1)) and fraction of dense fp16 MFMA peak.
+            (2 * D * Hq * S * (S+1)) and fraction of dense fp16 MFMA peak;
+            the cfg3 pipeline's other legs beside it: RoPE in place of q and
+            k, the paged KV store of the 2048 tokens, and the two fused.
   splitk    cfg4 long-context decode (B=8, ctx 32768): GB/s.
+  ref_harness  the reference's own decode harness shape (B=16, 32/32 heads,
+            ctx 2048, ascending tables; tests/test_paged_attention.py:12-125)
+            timed beside torch SDPA (fp16, contiguous K/V) on the same GPU.
   model     cfg5 Llama-3.2-3B random-init, B=8, prefill 512 then 128 greedy
             decode steps replayed via hipGraph: tok/s, ms/step, TTFT.
   cpu_baseline  the CPU oracle on the same cfg2 inputs, on this host's cores
-            (prefill and splitk carry their own, on cfg3 / cfg4; cfg5 has none:
-            an fp32 CPU forward of the 3B model is not a bounded sample).
+            (prefill, splitk and model carry their own: cfg3, cfg4, and a
+            bounded cfg5 sample -- B=8 prefill of 32 tokens then 4 greedy
+            steps of the fp32 model oracle).
 
   chunked   (--only chunked; not in the default run) chunked prefill from the
             page pool, B=1 chunk 512 behind 0-7680 cached tokens and B=4 chunk
             128 behind 2048, with and without the key split: us, TFLOP/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--only decode|prefill|splitk|model|chunked]
+                       [--only decode|prefill|splitk|harness|model|chunked]
 (--only runs one workload; only the default run prints the full result line.)
 """
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import platform
@@ -38,8 +45,9 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor spec
-TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                            "decode_hbm_traffic.json")
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_hbm_traffic.json")
+DECODE_SOURCE = os.path.join(ROOT, "mycustomcudaengine_amd", "csrc", "decode_attention.hip")
 FP16_DENSE_TFLOPS = 2500.0     # MI355X dense fp16 MFMA, vendor spec
 METRIC = "decode-attn HBM GB/s (% peak); prefill-attn TFLOPS (% MFMA); 3B decode tok/s"
 
@@ -132,6 +140,103 @@ def bench_prefill(case, dev, steps, warmup):
     return ms, flops, flops / (ms * 1e-3) / 1e12, graph_ms
 
 
+def bench_prefill_legs(case, dev, steps, warmup) -> dict:
+    """cfg3's other legs, each timed alone with HIP events over back-to-back
+    calls: RoPE in place of q [1, 2048, 24, 128] and k [1, 2048, 8, 128]
+    (theta 5e5, positions 0..2047), the paged KV store of the 2048 tokens'
+    k and v into a shuffled 16-token page pool (136 blocks, 128 used), and
+    the two fused in one launch (rope_kv_store).  Algorithmic bytes: RoPE
+    reads and writes q and k once and reads one cos and one sin row per token
+    (2048 x 64 x 4 B each) and the positions; the store reads k and v and
+    writes them once, plus the slots; the fused op rotates k in place and
+    also stores it."""
+    import my_cuda_engine_cpp as ops
+    from mycustomcudaengine_amd.engine.models.llama import rope_tables
+    from mycustomcudaengine_amd.ops import rope_kv_store
+    b, s, hq, hkv, d, bs = 1, 2048, 24, 8, 128, 16
+    q, k, v = case.query.to(dev), case.key.to(dev), case.value.to(dev)
+    cos, sin = rope_tables(4096, d, 500000.0, dev)
+    pos = torch.arange(s, dtype=torch.int32, device=dev).view(b, s)
+    nb = s // bs + 8
+    g = torch.Generator().manual_seed(44)
+    blocks = torch.randperm(nb, generator=g)[: s // bs].to(torch.int64)
+    t = torch.arange(s)
+    slots = (blocks[t // bs] * bs + t % bs).to(torch.int32).to(dev)
+    kc = torch.zeros(nb, bs, hkv, d, dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    qk_bytes = (q.numel() + k.numel()) * 2
+    table_bytes = 2 * s * (d // 2) * 4 + s * 4
+    kv_bytes = (k.numel() + v.numel()) * 2
+    rope_b = 2 * qk_bytes + table_bytes
+    store_b = 2 * kv_bytes + s * 4
+    # fused: q read and written, k read, written in place and to its page,
+    # v read and written to its page
+    fused_b = 2 * q.numel() * 2 + 3 * k.numel() * 2 + 2 * v.numel() * 2 + table_bytes + s * 4
+    out = {}
+    for name, fn, nbytes in (
+            ("rope_inplace", lambda: ops.rope_inplace(q, k, cos, sin, pos), rope_b),
+            ("paged_kv_store", lambda: ops.paged_kv_store(k.view(s, hkv, d), v.view(s, hkv, d),
+                                                          kc, vc, slots), store_b),
+            ("rope_kv_store", lambda: rope_kv_store(q.view(s, hq, d), k.view(s, hkv, d),
+                                                    v.view(s, hkv, d), kc, vc, cos, sin,
+                                                    pos.view(-1), slots), fused_b)):
+        ms = time_gpu(fn, steps, warmup)
+        out[name] = {"us": round(ms * 1e3, 2), "bytes": int(nbytes),
+                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        log(f"cfg3 {name}: {out[name]['us']} us, {out[name]['gbs']} GB/s")
+    return out
+
+
+def bench_harness(dev, steps: int, warmup: int) -> dict:
+    """The reference's decode harness shape (tests/test_paged_attention.py:12-125):
+    B=16, Hq = Hkv = 32, D=128, ctx 2048, 16-token blocks from KVCacheManager
+    (contiguous ascending tables), fp16 ~ N(0, 1).  paged_attention_decode is
+    timed beside torch.nn.functional.scaled_dot_product_attention on
+    contiguous [B, H, ctx, D] copies of the same K/V (the reference's
+    comparison, README.md:6), both with HIP events over back-to-back calls;
+    GB/s over the same algorithmic bytes (K and V once, q and out)."""
+    import my_cuda_engine_cpp as ops
+    from mycustomcudaengine_amd.engine.cache import KVCacheManager
+    b, h, d, ctx, bs = 16, 32, 128, 2048, 16
+    mgr = KVCacheManager(num_blocks=b * ctx // bs, block_size=bs, num_layers=1, num_heads=h,
+                         head_dim=d, device=dev)
+    for i in range(b):
+        mgr.allocate_sequence(i, ctx)
+    g = torch.Generator(device=dev).manual_seed(42)
+    mgr.kv_cache.normal_(generator=g)
+    q = torch.randn(b, h, d, generator=g, device=dev).half()
+    bt = mgr.get_block_table_tensor(list(range(b)), ctx // bs)
+    cl = torch.full((b,), ctx, dtype=torch.int32, device=dev)
+    kc, vc = mgr.kv_cache[0, 0], mgr.kv_cache[0, 1]
+    scale = d ** -0.5
+    nbytes = 2 * b * ctx * h * d * 2 + 2 * b * h * d * 2
+    ms = time_gpu(lambda: ops.paged_attention_decode(q, kc, vc, bt, cl, ctx // bs, bs, scale),
+                  steps, warmup)
+    out = {"workload": "reference decode harness: B=16, 32/32 heads, D=128, ctx 2048, "
+                       "ascending tables, fp16",
+           "us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+           "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    k = kc.view(b, ctx, h, d).transpose(1, 2).contiguous()
+    v = vc.view(b, ctx, h, d).transpose(1, 2).contiguous()
+    q4 = q.unsqueeze(2).contiguous()
+    try:
+        from torch.nn.attention import SDPBackend, sdpa_kernel
+        # fused backends only (no math fallback through batched GEMMs)
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            sms = time_gpu(lambda: torch.nn.functional.scaled_dot_product_attention(
+                q4, k, v, scale=scale), steps, warmup)
+        out["sdpa_us"] = round(sms * 1e3, 2)
+        out["sdpa_gbs"] = round(nbytes / (sms * 1e-3) / 1e9, 1)
+        out["speedup_vs_sdpa"] = round(sms / ms, 3)
+    except RuntimeError as e:  # no fused SDPA backend for this shape on this build
+        out["sdpa_us"] = None
+        out["sdpa_error"] = str(e)[:200]
+    log(f"reference harness: {out['us']} us ({out['gbs']} GB/s); SDPA {out.get('sdpa_us')} us")
+    del mgr, k, v
+    return out
+
+
 def bench_chunked(dev, steps: int, warmup: int) -> dict:
     """Chunked prefill attention from the page pool (ops.prefill_attention_paged):
     synthetic fp16 Q/K/V ~ N(0, 1), 24/8 heads, 16-token pages in a shuffled
@@ -165,7 +270,8 @@ def bench_chunked(dev, steps: int, warmup: int) -> dict:
     return out
 
 
-def bench_model(dev, steps: int = 128, batch: int = 8, prompt: int = 512, seed: int = 46) -> dict:
+def bench_model(dev, steps: int = 128, batch: int = 8, prompt: int = 512, seed: int = 46,
+                cpu: bool = True) -> dict:
     """cfg5: random-init Llama-3.2-3B (28 layers, fp16 weights ~ N(0, 0.02),
     RMSNorm weights 1, tied lm_head), B=8 prefill of 512 uniform-random token
     ids, then `steps` greedy decode steps replayed through the hipGraph runner.
@@ -249,6 +355,11 @@ def bench_model(dev, steps: int = 128, batch: int = 8, prompt: int = 512, seed: 
     step_ms = loop_s / steps * 1e3
     mean_ctx = prompt + 8 + steps + steps / 2  # positions of the timed device loop
     kv_bytes = batch * mean_ctx * cfg.num_hidden_layers * hkv * d * 2 * 2
+    cpu_base = None
+    if cpu:
+        del runner, cache
+        torch.cuda.empty_cache()
+        cpu_base = cpu_baseline_model(cfg, w, ids.cpu())
     return {"workload": "cfg5 Llama-3.2-3B random-init fp16, B=8, prefill 512, "
                         f"{steps} greedy decode steps replayed via hipGraph",
             "tok_s": round(batch * steps / loop_s, 1),
@@ -260,7 +371,47 @@ def bench_model(dev, steps: int = 128, batch: int = 8, prompt: int = 512, seed: 
             "bytes_per_step": int(weight_bytes + kv_bytes),
             "gbs": round((weight_bytes + kv_bytes) / (step_ms * 1e-3) / 1e9, 1),
             "frac_of_hbm_peak": round((weight_bytes + kv_bytes) / (step_ms * 1e-3) / 1e9
-                                      / HBM_PEAK_GBS, 4)}
+                                      / HBM_PEAK_GBS, 4),
+            "cpu_baseline": cpu_base}
+
+
+def cpu_baseline_model(cfg, weights: dict, ids: torch.Tensor, prompt: int = 32,
+                       steps: int = 4) -> dict:
+    """A bounded cfg5 sample on the CPU: the fp32 model oracle (oracle/model_ref.py)
+    with the benchmark's own weights (copied to the host as fp32) prefills the
+    first `prompt` tokens of the benchmark's 8 prompts, then takes `steps`
+    greedy decode steps.  value = decode tokens/s (8 sequences x steps over the
+    decode wall time); the prefill time is reported beside it."""
+    from oracle.model_ref import LlamaRef
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    hf = dict(hidden_size=cfg.hidden_size, intermediate_size=cfg.intermediate_size,
+              num_hidden_layers=cfg.num_hidden_layers,
+              num_attention_heads=cfg.num_attention_heads,
+              num_key_value_heads=cfg.num_key_value_heads, head_dim=cfg.head_dim,
+              vocab_size=cfg.vocab_size, rms_norm_eps=cfg.rms_norm_eps, rope_theta=cfg.rope_theta)
+    names = [k for k in weights if not k.startswith("lm_head")]
+    ref = LlamaRef(hf, {k: weights[k] for k in names})
+    b = ids.shape[0]
+    seq = list(range(b))
+    t0 = time.perf_counter()
+    logits = ref.prefill(ids[:, :prompt], seq)
+    prefill_s = time.perf_counter() - t0
+    tok = logits.argmax(-1, keepdim=True)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        logits = ref.decode(tok, [prompt + i] * b, seq)
+        tok = logits.argmax(-1, keepdim=True)
+    decode_s = time.perf_counter() - t0
+    info = cpu_info()
+    return {"value": round(b * steps / decode_s, 3), "unit": "tok/s", "cores": n, "kind": "port",
+            "prefill_ms": round(prefill_s * 1e3, 1),
+            "ms_per_step": round(decode_s / steps * 1e3, 1),
+            "sample": f"cfg5 geometry with the benchmark's weights, fp32 torch model oracle: "
+                      f"B={b} prefill of {prompt} tokens ({prefill_s * 1e3:.0f} ms), then "
+                      f"{steps} greedy decode steps ({decode_s / steps * 1e3:.0f} ms/step, "
+                      f"positions {prompt}-{prompt + steps - 1}); {info['cpu_model']}; "
+                      f"torch {info['torch']}"}
 
 
 def cpu_baseline_decode(case) -> dict:
@@ -310,10 +461,12 @@ def cpu_baseline_prefill(case) -> dict:
     from oracle.ops_ref import prefill_attention_ref
     med, n = cpu_median_s(lambda: prefill_attention_ref(case.query, case.key, case.value,
                                                         case.scale))
+    info = cpu_info()
     return {"value": round(case.algorithmic_flops() / med / 1e12, 4), "unit": "TFLOP/s",
             "cores": len(os.sched_getaffinity(0)), "kind": "port",
             "sample": f"full cfg3 (B=1, S=2048), fp32 torch oracle, median of {n} runs after "
-                      f"1 warmup, {med * 1e3:.1f} ms/run"}
+                      f"1 warmup, {med * 1e3:.1f} ms/run; {info['cpu_model']}; "
+                      f"torch {info['torch']}"}
 
 
 def cpu_baseline_splitk(case) -> dict:
@@ -322,19 +475,30 @@ def cpu_baseline_splitk(case) -> dict:
     med, n = cpu_median_s(lambda: decode_attention_ref(
         case.query, case.key_cache, case.value_cache, case.block_tables, case.context_lens,
         case.scale))
+    info = cpu_info()
     return {"value": round(case.algorithmic_bytes() / med / 1e9, 3), "unit": "GB/s",
             "cores": len(os.sched_getaffinity(0)), "kind": "port",
             "sample": f"full cfg4 (B=8, ctx 32768), fp32 torch oracle, median of {n} runs after "
-                      f"1 warmup, {med * 1e3:.1f} ms/run"}
+                      f"1 warmup, {med * 1e3:.1f} ms/run; {info['cpu_model']}; "
+                      f"torch {info['torch']}"}
+
+
+def source_sha(path: str = DECODE_SOURCE) -> str:
+    with open(path, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
 
 
 def measured_traffic():
     """HBM bytes per decode-kernel launch from the committed rocprofv3
     FETCH_SIZE/WRITE_SIZE passes (calibrated against a 256 MiB copy), or None
-    when that summary is absent."""
+    when that summary is absent or was collected on another version of the
+    decode kernel source (its recorded sha256 prefix differs)."""
     try:
         with open(TRAFFIC_FILE) as f:
-            return int(json.load(f)["traffic_bytes_per_launch"])
+            rec = json.load(f)
+        if rec.get("decode_source_sha16") != source_sha():
+            return None
+        return int(rec["traffic_bytes_per_launch"])
     except (OSError, KeyError, ValueError):
         return None
 
@@ -345,7 +509,8 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "prefill", "splitk", "model", "chunked"],
+    ap.add_argument("--only", choices=["decode", "prefill", "splitk", "harness", "model",
+                                       "chunked"],
                     default=None)
     ap.add_argument("--calibration-copy", action="store_true",
                     help="first copy 256 MiB device-to-device (a kernel of known traffic, "
@@ -395,6 +560,7 @@ def main() -> None:
                             "frac_of_fp16_dense_peak": round(tfs / FP16_DENSE_TFLOPS, 4),
                             "timing": "back-to-back eager calls, HIP events",
                             "graph_replay_us": round(pgms * 1e3, 2)}
+        extra["prefill"]["legs"] = bench_prefill_legs(case3, dev, max(20, args.steps // 4), 5)
         if not args.no_cpu:
             extra["prefill"]["cpu_baseline"] = cpu_baseline_prefill(case3)
             log(f"cfg3 CPU baseline: {extra['prefill']['cpu_baseline']['value']} TFLOP/s")
@@ -413,9 +579,15 @@ def main() -> None:
         del case4
         torch.cuda.empty_cache()
 
+    if args.only in (None, "harness"):
+        extra["ref_harness"] = bench_harness(dev, max(20, args.steps // 4), 5)
+        torch.cuda.empty_cache()
+
     if args.only in (None, "model"):
         log("cfg5 Llama-3.2-3B decode")
-        extra["model"] = bench_model(dev)
+        extra["model"] = bench_model(dev, cpu=not args.no_cpu)
+        if extra["model"]["cpu_baseline"]:
+            log(f"cfg5 CPU baseline: {extra['model']['cpu_baseline']['value']} tok/s")
         log(f"cfg5 model: {extra['model']['tok_s']} tok/s, {extra['model']['ms_per_step']} ms/step "
             f"(host-prepared steps: {extra['model']['tok_s_host_prepared']} tok/s)")
         torch.cuda.empty_cache()

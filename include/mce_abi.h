@@ -119,7 +119,10 @@ MCE_API size_t mce_paged_attention_decode_workspace_size(int batch, int num_head
  * Workspace: 256-byte aligned, at least
  * mce_paged_attention_decode_workspace_size() bytes, no initialisation
  * needed; it is scratch for the duration of the call (two calls that run
- * concurrently need two workspaces).
+ * concurrently need two workspaces).  It holds (J + batch) partial-state
+ * slots of 520 bytes per query head, J ~ one workgroup per CU per group of
+ * 8 kv heads (3.6 MB for 32 sequences x 24 heads on 256 CUs), whatever the
+ * context lengths.
  * Replaces paged_attention_decode_cuda (csrc/kernels/flash_attn_paged.cu:
  * 144-168; binding csrc/bindings.cpp:8,26).
  */

@@ -29,7 +29,12 @@
 //   A sequence that lies inside one workgroup is normalised and written
 //   directly; otherwise each segment writes its partial softmax state (max m,
 //   sum l, unnormalised acc[128]) to the workspace and a second kernel merges
-//   the partials of each (sequence, query head) by log-sum-exp.  (Merging in
+//   the partials of each (sequence, query head) by log-sum-exp.  Partial slots
+//   are compact: workgroup j writes its piece of sequence b to slot j + b of
+//   each query head's row of J + B slots.  (The pieces of b sit in workgroups
+//   j_first(b) .. j_last(b) and j_first(b') >= j_last(b) for b' > b, so the
+//   slot ranges [j_first(b) + b, j_last(b) + b] never overlap.)  Workgroup 0
+//   records each sequence's first slot and part count for the merge.  (Merging in
 //   the last-arriving workgroup would need agent-scope release/acquire
 //   fences, which on gfx950 write back the L2 per workgroup; the kernel
 //   boundary gives the same visibility for free.)
@@ -77,11 +82,11 @@ struct DecodeArgs {
   const int32_t *btab;      // [B, maxb]
   const int32_t *ctx_lens;  // [B]
   uint16_t *out;            // [B, Hq, HD]
-  float *ws_ml;             // [B, Hq, P, 2]
-  float *ws_acc;            // [B, Hq, P, HD]
-  int *ws_nparts;           // [B] workgroups covering each sequence
+  float *ws_ml;             // [Hq, S, 2]
+  float *ws_acc;            // [Hq, S, HD]
+  int *ws_meta;             // [B, 2]: first slot and part count of each sequence
   int B, Hq, Hkv, maxb, bs_log2, J;
-  int P;                    // part slots per row: min(J, table tiles) (a part holds >= 1 tile)
+  int S;                    // part slots per query head: J + B
   int hpg, wph;             // kv heads per workgroup, waves per kv head
   int per_seq;              // 1: workgroup (group, b) covers all of sequence b
   int64_t q_stride_b;       // elements between the query rows of two sequences
@@ -299,11 +304,15 @@ void paged_decode_kernel(DecodeArgs a) {
         for (int i = tid; i < (h_hi - h_lo) * HD; i += NTH)
           a.out[((int64_t)b * a.Hq + h_lo) * HD + i] = 0;
     if (hgrp == 0)
-      for (int b = tid; b < a.B; b += NTH)
-        a.ws_nparts[b] = pre[b + 1] == pre[b]
-                             ? 0
-                             : owner_of(pre[b + 1] - 1, NT, je) -
-                                   owner_of(pre[b] + seg0, NT, je) + 1;
+      for (int b = tid; b < a.B; b += NTH) {
+        int first = 0, n = 0;
+        if (pre[b + 1] != pre[b]) {
+          const int jf = owner_of(pre[b] + seg0, NT, je);
+          first = jf + b;
+          n = owner_of(pre[b + 1] - 1, NT, je) - jf + 1;
+        }
+        *reinterpret_cast<int2 *>(a.ws_meta + 2 * b) = int2{first, n};
+      }
   }
   if (!a.per_seq && j >= je) return;
   const int t_lo = a.per_seq ? 0 : range_start(j, NT, je);
@@ -556,7 +565,7 @@ void paged_decode_kernel(DecodeArgs a) {
       }
     }
     const int64_t row0 = (int64_t)b * a.Hq + head0;
-    const int slot = j - j_first;
+    const int slot = j + b;  // this piece's partial slot (compact layout)
     if (wph == 1) {
       // the wave owns its kv head: write the final rows or this segment's
       // partial state directly (lanes 0-15 hold dims 8 lr .. 8 lr + 7)
@@ -571,7 +580,7 @@ void paged_decode_kernel(DecodeArgs a) {
               o[k] = pack2<T>(acc[h][2 * k] * inv, acc[h][2 * k + 1] * inv);
             *reinterpret_cast<u32x4 *>(a.out + (row0 + h) * HD + lr * 8) = o;
           } else {
-            const int64_t pr = (row0 + h) * a.P + slot;
+            const int64_t pr = (int64_t)(head0 + h) * a.S + slot;
             float *dst = a.ws_acc + pr * HD + lr * 8;
             *reinterpret_cast<floatx4 *>(dst) =
                 floatx4{acc[h][0], acc[h][1], acc[h][2], acc[h][3]};
@@ -617,11 +626,12 @@ void paged_decode_kernel(DecodeArgs a) {
         L += red_l[hh + r * hpg][h] * sc;
         A += red_acc[hh + r * hpg][h][d] * sc;
       }
-      const int64_t row = (int64_t)b * a.Hq + (hgrp * hpg + hh) * gq + gsub * G + h;
+      const int hidx = (hgrp * hpg + hh) * gq + gsub * G + h;
+      const int64_t row = (int64_t)b * a.Hq + hidx;
       if (nparts == 1) {
         a.out[row * HD + d] = T::from_float(A / L);
       } else {
-        const int64_t pr = row * a.P + slot;
+        const int64_t pr = (int64_t)hidx * a.S + slot;
         a.ws_acc[pr * HD + d] = A;
         if (d == 0) {
           a.ws_ml[pr * 2] = M;
@@ -641,20 +651,19 @@ template <class T>
 __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int64_t row = (int64_t)b * a.Hq + h;
-  const float *ml = a.ws_ml + row * a.P * 2;
-  const float *ac = a.ws_acc + row * a.P * HD + d;
-  // The part count, the first HD parts' (m, l) and this lane's dim of the
-  // first SPEC parts' partial outputs are loaded together (one memory round
-  // trip); slots at or past the count are never used (the workspace holds
-  // P >= parts slots per row, so these reads stay inside it).
+  const int2 meta = *reinterpret_cast<const int2 *>(a.ws_meta + 2 * b);
+  const int n = __builtin_amdgcn_readfirstlane(meta.y);
+  if (n <= 1) return;
+  const int first = __builtin_amdgcn_readfirstlane(meta.x);
+  const float *ml = a.ws_ml + ((int64_t)h * a.S + first) * 2;
+  const float *ac = a.ws_acc + ((int64_t)h * a.S + first) * HD + d;
+  // The first HD parts' (m, l) and this lane's dim of the first SPEC parts'
+  // partial outputs are loaded together (one memory round trip).
   constexpr int SPEC = 16;
-  const int n_raw = a.ws_nparts[b];
-  const float2 ml0 = d < a.P ? *reinterpret_cast<const float2 *>(ml + 2 * d) : float2{0.f, 0.f};
+  const float2 ml0 = d < n ? *reinterpret_cast<const float2 *>(ml + 2 * d) : float2{0.f, 0.f};
   float v0[SPEC];
 #pragma unroll
-  for (int k = 0; k < SPEC; ++k) v0[k] = k < a.P ? ac[(int64_t)k * HD] : 0.f;
-  const int n = __builtin_amdgcn_readfirstlane(n_raw);
-  if (n <= 1) return;
+  for (int k = 0; k < SPEC; ++k) v0[k] = k < n ? ac[(int64_t)k * HD] : 0.f;
   __shared__ float w_lds[HD], wl_lds[HD], mx_lds[2];
   float M = -INFINITY, L = 0.f, A = 0.f;
   for (int c0 = 0; c0 < n; c0 += HD) {
@@ -711,28 +720,26 @@ __global__ __launch_bounds__(HD) void paged_decode_merge_kernel(DecodeArgs a) {
 }
 
 struct DecodeLayout {
-  int J, P, hpg, wph, groups;
-  size_t ml_off, acc_off, nparts_off, total;
+  int J, S, hpg, wph, groups;
+  size_t ml_off, acc_off, meta_off, total;
 };
 
-// P: part slots per (sequence, query head) row.  Every workgroup range holds
-// at least one tile, so a sequence of T tiles has at most T parts, and T is
-// at most the table capacity in tiles.
-static DecodeLayout decode_layout(int batch, int num_heads, int num_kv_heads, int64_t cap_tokens) {
+// S = J + B part slots per query head (compact layout: piece of sequence b in
+// workgroup j at slot j + b), then two ints per sequence (first slot, parts).
+static DecodeLayout decode_layout(int batch, int num_heads, int num_kv_heads) {
   DecodeLayout L{};
   L.hpg = num_kv_heads < DEC_NW ? num_kv_heads : DEC_NW;
   L.wph = DEC_NW / L.hpg;
   L.groups = (num_kv_heads + L.hpg - 1) / L.hpg;
   int J = cu_count() / L.groups;
   L.J = J < 1 ? 1 : (J > 512 ? 512 : J);
-  const int64_t cap_tiles = (cap_tokens + TILE - 1) / TILE;
-  L.P = (int)(cap_tiles < L.J ? (cap_tiles < 1 ? 1 : cap_tiles) : L.J);
+  L.S = L.J + batch;
   auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
-  const size_t rows = (size_t)batch * num_heads * L.P;
+  const size_t rows = (size_t)num_heads * L.S;
   L.ml_off = 0;
   L.acc_off = up(rows * 2 * sizeof(float));
-  L.nparts_off = up(L.acc_off + rows * HD * sizeof(float));
-  L.total = L.nparts_off + up((size_t)batch * sizeof(int));
+  L.meta_off = up(L.acc_off + rows * HD * sizeof(float));
+  L.total = L.meta_off + up((size_t)batch * 2 * sizeof(int));
   return L;
 }
 
@@ -748,8 +755,7 @@ extern "C" size_t mce_paged_attention_decode_workspace_size(
     return 0;
   // short contexts run the per-sequence mode, which needs no workspace
   if ((int64_t)max_blocks_per_seq * block_size <= PER_SEQ_MAX_TOKENS) return 0;
-  return decode_layout(batch, num_heads, num_kv_heads,
-                       (int64_t)max_blocks_per_seq * block_size).total;
+  return decode_layout(batch, num_heads, num_kv_heads).total;
 }
 
 namespace {
@@ -800,8 +806,7 @@ int decode_impl(int dtype, const void *query, const void *key_cache, const void 
   MCE_REQUIRE((int64_t)batch * ((int64_t)max_blocks_per_seq * block_size / TILE + 1) <
                   ((int64_t)1 << 30),
               "mce_paged_attention_decode: batch x context too large");
-  const DecodeLayout Lay = decode_layout(batch, num_heads, num_kv_heads,
-                                         (int64_t)max_blocks_per_seq * block_size);
+  const DecodeLayout Lay = decode_layout(batch, num_heads, num_kv_heads);
   const bool per_seq = (int64_t)max_blocks_per_seq * block_size <= PER_SEQ_MAX_TOKENS;
   if (!per_seq && (workspace == nullptr || workspace_bytes < Lay.total ||
                    (reinterpret_cast<uintptr_t>(workspace) & 255) != 0))
@@ -829,14 +834,14 @@ int decode_impl(int dtype, const void *query, const void *key_cache, const void 
   char *base = (char *)workspace;  // unused (may be null) in per-sequence mode
   a.ws_ml = per_seq ? nullptr : (float *)(base + Lay.ml_off);
   a.ws_acc = per_seq ? nullptr : (float *)(base + Lay.acc_off);
-  a.ws_nparts = per_seq ? nullptr : (int *)(base + Lay.nparts_off);
+  a.ws_meta = per_seq ? nullptr : (int *)(base + Lay.meta_off);
   a.B = batch;
   a.Hq = num_heads;
   a.Hkv = num_kv_heads;
   a.maxb = max_blocks_per_seq;
   a.bs_log2 = ilog2(block_size);
   a.J = Lay.J;
-  a.P = Lay.P;
+  a.S = Lay.S;
   a.hpg = Lay.hpg;
   a.wph = Lay.wph;
   // Short contexts: one workgroup per (kv head, sequence) streams the whole

@@ -24,7 +24,100 @@ __device__ inline bool am_better(float a, int64_t ia, float b, int64_t ib) {
   return a > b || (a == b && ia < ib);
 }
 
-// one workgroup per row
+// Order key of argmax's value rule as an unsigned integer: larger keys are
+// larger values, NaN (any sign or payload) above +inf, -0 equal to +0 (equal
+// values are then ranked by index alone, as torch.argmax does).
+__device__ inline uint32_t am_key(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  if (v != v) return 0xffffffffu;
+  if ((u << 1) == 0) return 0x80000000u;  // +0 and -0
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+// (key, index) order: larger key first, the lower index among equals.
+__device__ inline bool am_key_better(uint32_t ka, int ia, uint32_t kb, int ib) {
+  return ka > kb || (ka == kb && ia < ib);
+}
+
+// One workgroup of AMV_THREADS per row, 16-byte loads: every thread has
+// AMV_CHUNKS loads of 8 values in flight at once (a 128256-wide fp16 row is
+// one pass), scans them in increasing column order keeping the first
+// largest, and the workgroup reduces (key, index) pairs by the order above.
+// Rows must start 16-byte aligned; cols < 2^31.
+constexpr int AMV_THREADS = 1024;
+constexpr int AMV_CHUNKS = 16;
+
+template <class T>
+__global__ __launch_bounds__(AMV_THREADS) void argmax_rows_vec_kernel(
+    const uint16_t *__restrict__ x, int cols, int64_t stride, int64_t *__restrict__ out) {
+  const uint16_t *xr = x + (int64_t)blockIdx.x * stride;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  uint32_t bk = 0;  // below every value's key
+  int bi = cols;    // past the end: loses to every real element
+  const int n8 = cols >> 3;
+  for (int base = 0; base < n8; base += AMV_THREADS * AMV_CHUNKS) {
+    u32x4 v[AMV_CHUNKS];
+#pragma unroll
+    for (int k = 0; k < AMV_CHUNKS; ++k) {
+      const int c8 = base + k * AMV_THREADS + tid;
+      v[k] = c8 < n8 ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(xr) + c8)
+                     : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int k = 0; k < AMV_CHUNKS; ++k) {
+      const int c8 = base + k * AMV_THREADS + tid;
+      if (c8 < n8) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t k0 = am_key(T::lo(v[k][e])), k1 = am_key(T::hi(v[k][e]));
+          if (k0 > bk) {
+            bk = k0;
+            bi = c8 * 8 + 2 * e;
+          }
+          if (k1 > bk) {
+            bk = k1;
+            bi = c8 * 8 + 2 * e + 1;
+          }
+        }
+      }
+    }
+  }
+  const int c = n8 * 8 + tid;  // columns past the last whole 8-value chunk
+  if (c < cols) {
+    const uint32_t kc = am_key(T::lo(xr[c]));
+    if (am_key_better(kc, c, bk, bi)) {
+      bk = kc;
+      bi = c;
+    }
+  }
+  // the order is total, so the reduction order does not change the result
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const uint32_t ok = (uint32_t)__shfl_xor((int)bk, d, 64);
+    const int oi = __shfl_xor(bi, d, 64);
+    if (am_key_better(ok, oi, bk, bi)) {
+      bk = ok;
+      bi = oi;
+    }
+  }
+  __shared__ uint32_t wk[AMV_THREADS / 64];
+  __shared__ int wi[AMV_THREADS / 64];
+  if (lane == 0) {
+    wk[w] = bk;
+    wi[w] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int k = 1; k < AMV_THREADS / 64; ++k)
+      if (am_key_better(wk[k], wi[k], bk, bi)) {
+        bk = wk[k];
+        bi = wi[k];
+      }
+    out[blockIdx.x] = bi < cols ? bi : 0;
+  }
+}
+
+// one workgroup per row, 2-byte loads (rows that are not 16-byte aligned)
 template <class T>
 __global__ __launch_bounds__(AM_THREADS) void argmax_rows_kernel(const uint16_t *__restrict__ x,
                                                                  int64_t cols, int64_t stride,
@@ -106,7 +199,14 @@ extern "C" int mce_argmax_rows(int dtype, const void *logits, int64_t rows, int6
   MCE_REQUIRE(logits && out, "mce_argmax_rows: null pointer");
   MCE_REQUIRE(rows < ((int64_t)1 << 31), "mce_argmax_rows: too many rows");
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == MCE_F16)
+  if (aligned16(logits) && row_stride % 8 == 0 && cols < ((int64_t)1 << 31)) {
+    if (dtype == MCE_F16)
+      argmax_rows_vec_kernel<F16T><<<(unsigned)rows, AMV_THREADS, 0, st>>>(
+          (const uint16_t *)logits, (int)cols, row_stride, out);
+    else
+      argmax_rows_vec_kernel<BF16T><<<(unsigned)rows, AMV_THREADS, 0, st>>>(
+          (const uint16_t *)logits, (int)cols, row_stride, out);
+  } else if (dtype == MCE_F16)
     argmax_rows_kernel<F16T><<<(unsigned)rows, AM_THREADS, 0, st>>>((const uint16_t *)logits, cols,
                                                                     row_stride, out);
   else

@@ -104,17 +104,22 @@ def test_decode_workspace_size(lib):
     assert 0 < small < big
     assert big % 256 == 0
 
-    # rows of P = min(J, table tiles) part slots: (m, l) and 128 partial dims in
-    # fp32, then the per-sequence part counts; J = 256 workgroups (no GPU: 256
-    # CUs assumed, one group of 8 kv heads)
-    def expect(b, hq, cap_tokens):
+    # J + B compact part slots per query head: (m, l) and 128 partial dims in
+    # fp32, then (first slot, part count) per sequence; J = one workgroup per CU
+    # for one group of 8 kv heads (the library assumes 256 CUs without a GPU)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count \
+        if torch.cuda.is_available() else 256
+
+    def expect(b, hq, groups=1):
         up = lambda x: (x + 255) // 256 * 256
-        p = min(256, (cap_tokens + 31) // 32)
-        rows = b * hq * p
-        return up(rows * 2 * 4) + up(rows * 128 * 4) + up(b * 4)
-    assert big == expect(32, 24, 256 * 16)          # cfg2: 128 slots
-    assert f(8, 24, 8, 2048, 16) == expect(8, 24, 2048 * 16)   # cfg4: J = 256 slots
-    assert f(32, 24, 8, 100, 16) == expect(32, 24, 1600)       # 50 slots
+        rows = hq * (min(512, max(1, cus // groups)) + b)
+        return up(rows * 2 * 4) + up(rows * 128 * 4) + up(b * 8)
+    assert big == expect(32, 24)                                # cfg2
+    assert f(8, 24, 8, 2048, 16) == expect(8, 24)               # cfg4
+    assert f(32, 24, 8, 100, 16) == expect(32, 24)              # independent of the width
+    assert f(16, 32, 32, 128, 16) == expect(16, 32, groups=4)   # 32 kv heads: 4 groups
+    if cus == 256:
+        assert big < 4 * 2 ** 20                                # 3.6 MB at cfg2
 
 
 def test_rope_and_prefill_validation(lib):

@@ -50,6 +50,44 @@ def test_cfg4_long_context_split_k(dev):
     check(cfg4_decode(), dev)
 
 
+def reference_harness_case(dev):
+    """The reference's own decode test shape (tests/test_paged_attention.py:12-54):
+    B=16, Hq = Hkv = 32 (no GQA), D=128, ctx 2048, 16-token blocks from
+    KVCacheManager (contiguous ascending tables), Q/K/V ~ N(0, 1) fp16 drawn
+    with a seeded CPU generator."""
+    from mycustomcudaengine_amd.engine.cache import KVCacheManager
+    b, h, d, ctx, bs = 16, 32, 128, 2048, 16
+    mgr = KVCacheManager(num_blocks=b * ctx // bs, block_size=bs, num_layers=1, num_heads=h,
+                         head_dim=d, device=dev)
+    for s in range(b):
+        mgr.allocate_sequence(s, ctx)
+    g = torch.Generator().manual_seed(42)
+    mgr.kv_cache.copy_(torch.randn(mgr.kv_cache.shape, generator=g).half())
+    q = torch.randn(b, h, d, generator=g).half()
+    bt = mgr.get_block_table_tensor(list(range(b)), ctx // bs)
+    cl = torch.full((b,), ctx, dtype=torch.int32)
+    return q, mgr.kv_cache[0, 0], mgr.kv_cache[0, 1], bt, cl, ctx // bs, bs, 1.0 / math.sqrt(d)
+
+
+def test_reference_harness_shape(dev):
+    """The reference's decode harness (B=16, 32/32 heads, ctx 2048, ascending
+    tables): max-abs 1e-2 of the fp32 oracle, and the reference's own check,
+    allclose(atol=1e-2, rtol=1e-2) against fp16 SDPA on contiguous copies
+    (tests/test_paged_attention.py:65-86), here computed on the CPU."""
+    q, kc, vc, bt, cl, mb, bs, scale = reference_harness_case(dev)
+    assert bt.cpu().view(-1).tolist() == list(range(16 * mb))  # contiguous ascending
+    out = ops.paged_attention_decode(q.to(dev), kc, vc, bt, cl.to(dev), mb, bs, scale).cpu()
+    ref = decode_attention_ref(q, kc.cpu(), vc.cpu(), bt.cpu(), cl, scale)
+    assert (out.float() - ref).abs().max().item() <= TOL
+    # the reference's fp16 SDPA check, run on the CPU
+    k = kc.cpu().view(16, 2048, 32, 128).transpose(1, 2).contiguous()
+    v = vc.cpu().view(16, 2048, 32, 128).transpose(1, 2).contiguous()
+    sdpa = torch.nn.functional.scaled_dot_product_attention(q.unsqueeze(2), k, v,
+                                                            scale=scale).squeeze(2)
+    assert sdpa.dtype == torch.float16
+    assert torch.allclose(out, sdpa, atol=1e-2, rtol=1e-2)
+
+
 @pytest.mark.parametrize("ctx", [1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129,
                                  255, 256, 257, 511, 513, 1000, 1024, 1025, 2049])
 def test_context_edges(dev, ctx):

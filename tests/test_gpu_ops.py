@@ -411,14 +411,20 @@ def test_decode_gemm_rejects_unsupported_shapes(dev):
 
 # ------------------------------------------------ device-side decode loop
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("rows,cols", [(8, 128256), (3, 1000), (1, 1)])
-def test_argmax_rows_matches_torch(dev, dtype, rows, cols):
+@pytest.mark.parametrize("rows,cols,stride", [(8, 128256, 128256), (3, 1000, 1008),
+                                              (4, 1003, 1008), (2, 300007, 300016),
+                                              (3, 1000, 1011), (1, 1, 9)])
+def test_argmax_rows_matches_torch(dev, dtype, rows, cols, stride):
     """Greedy tokens equal torch.argmax (and the numpy oracle) exactly,
-    including rows whose maximum repeats and a row with NaNs; strided rows."""
+    including rows whose maximum repeats, a row with NaNs and a row whose
+    maximum is a -0 / +0 tie; strided rows.  Row strides that are multiples of
+    8 take the 16-byte-load kernel (with a tail when cols % 8 != 0, and more
+    than one pass per thread past 131072 columns), other strides the scalar
+    one."""
     from mycustomcudaengine_amd.ops import argmax_rows
     from oracle.alloc_ref import argmax_rows_ref
-    g = gen(150 + rows)
-    buf = (torch.randn(rows, cols + 8, generator=g) * 4).to(dtype)
+    g = gen(150 + rows + cols % 7)
+    buf = (torch.randn(rows, stride, generator=g) * 4).to(dtype)
     x = buf[:, :cols]
     if cols > 10:
         x[0, cols // 3] = x[0].max() + 1
@@ -426,6 +432,10 @@ def test_argmax_rows_matches_torch(dev, dtype, rows, cols):
         if rows > 1:
             x[1, 5] = float("nan")
             x[1, cols - 3] = float("nan")          # NaN ranks first, first NaN wins
+        if rows > 2:
+            x[2] = -x[2].abs() - 1
+            x[2, 7] = -0.0
+            x[2, cols - 1] = 0.0                    # equal to -0: index 7 wins
     got = argmax_rows(buf.to(dev)[:, :cols]).cpu()
     assert got.tolist() == torch.argmax(x.float(), dim=-1).tolist()
     assert got.tolist() == argmax_rows_ref(x.float().numpy()).tolist()

@@ -263,9 +263,10 @@ def test_argmax_rows_ref_tie_and_nan_rules():
     x = np.array([[1.0, 3.0, 3.0, -2.0],     # first of equal maxima
                   [-np.inf, -np.inf, -5.0, -5.0],
                   [0.0, np.nan, 7.0, np.nan],  # NaN above every number, first NaN
-                  [2.0, 2.0, 2.0, 2.0]], np.float32)
+                  [2.0, 2.0, 2.0, 2.0],
+                  [-1.0, -0.0, 0.0, -2.0]], np.float32)  # -0 equals +0: the first wins
     got = argmax_rows_ref(x)
-    assert got.tolist() == [1, 2, 1, 0]
+    assert got.tolist() == [1, 2, 1, 0, 1]
     assert got.tolist() == torch.argmax(torch.from_numpy(x), dim=-1).tolist()
 
 
