@@ -137,6 +137,32 @@ MCE_API int mce_paged_attention_decode(int dtype, const void *query,
                                void *stream);
 
 /*
+ * mce_paged_attention_decode without the workspace argument: the split-K
+ * partials go to a static scratch array of the library (file scope, 256-byte
+ * aligned, MCE_DECODE_NOALLOC_SCRATCH_BYTES = 16 MiB, one copy per GPU the
+ * library runs on, held until the process ends), so the call allocates
+ * nothing.  Same arguments, results (bit for bit) and
+ * validation otherwise.  Shapes whose workspace
+ * (mce_paged_attention_decode_workspace_size) exceeds the scratch return
+ * MCE_ERR_UNSUPPORTED.  Calls that overlap on one GPU share the scratch and
+ * race: serialise them (one stream, or one call at a time).  The first call
+ * on each device looks the scratch up with hipGetSymbolAddress; make it
+ * outside stream capture.  No counterpart in the reference: for callers that
+ * cannot allocate (code under HIP graph capture that must not touch the
+ * allocator, tight serving loops, harnesses that forbid hipMalloc).
+ */
+#define MCE_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+
+MCE_API int mce_paged_attention_decode_noalloc(int dtype, const void *query,
+                                       const void *key_cache, const void *value_cache,
+                                       const int32_t *block_tables,
+                                       const int32_t *context_lens, void *output,
+                                       int batch, int num_heads, int num_kv_heads,
+                                       int head_dim, int max_blocks_per_seq,
+                                       int block_size, int64_t num_blocks, float scale,
+                                       void *stream);
+
+/*
  * One decode token per sequence with the rotary embedding and the paged
  * store of the new token fused in: rotates query[b] and key[b] at
  * positions[b] (rows of cos/sin_table as in mce_rope_inplace; positions

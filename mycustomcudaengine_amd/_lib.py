@@ -27,6 +27,7 @@ MCE_ERR_LAUNCH = 3
 MCE_ERR_WORKSPACE = 4
 MCE_F16 = 0
 MCE_BF16 = 1
+MCE_DECODE_NOALLOC_SCRATCH_BYTES = 16 << 20
 
 _c_int, _c_i64, _c_f, _c_sz, _vp = (
     ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p)
@@ -43,6 +44,9 @@ SIGNATURES = {
     "mce_paged_attention_decode": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_int,
                                             _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64,
                                             _c_f, _vp, _c_sz, _vp]),
+    "mce_paged_attention_decode_noalloc": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_int,
+                                                    _c_int, _c_int, _c_int, _c_int, _c_int,
+                                                    _c_i64, _c_f, _vp]),
     "mce_rope_inplace": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int,
                                   _c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
                                   _c_i64, _c_i64, _vp]),

@@ -53,6 +53,8 @@
 //   * online softmax in base 2 (p = exp2((s - m) c), c = scale log2 e);
 //   * P V with v_dot2 over token pairs (p packed as fp16 / bf16), from the
 //     same registers -- no LDS round trip for p.
+#include <mutex>
+
 #include "mce_common.h"
 
 namespace mce {
@@ -909,6 +911,72 @@ extern "C" int mce_paged_attention_decode(
   return decode_impl(dtype, query, key_cache, value_cache, block_tables, context_lens, output,
                      batch, num_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size,
                      num_blocks, scale, workspace, workspace_bytes, stream, FusedRope{});
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the split-K partials live in a file-scope device
+// array instead of a caller workspace.  Every GPU the library runs on holds
+// its own copy (DECODE_SCRATCH_BYTES) until the process ends; its address on
+// each device is fetched once, with that device current, by
+// hipGetSymbolAddress, and only that address is handed to kernels (the
+// array's name is a host-side stand-in in host code).  The partials need no
+// initialisation (workgroup 0 writes the per-sequence part counts before the
+// merge kernel reads them), so nothing is cleared between calls.  Calls that
+// overlap on one GPU share the array and race.
+constexpr size_t DECODE_SCRATCH_BYTES = MCE_DECODE_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[DECODE_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[MAX_DEVICES] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device).
+int scratch_address(void **out) {
+  int dev = -1;
+  const hipError_t ge = hipGetDevice(&dev);
+  if (ge != hipSuccess || dev < 0 || dev >= MAX_DEVICES)
+    return set_error(MCE_ERR_LAUNCH, "mce_paged_attention_decode_noalloc: no current device (%s)",
+                     hipGetErrorString(ge));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return set_error(MCE_ERR_LAUNCH,
+                       "mce_paged_attention_decode_noalloc: hipGetSymbolAddress(scratch) failed "
+                       "on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return MCE_OK;
+}
+}  // namespace
+
+extern "C" int mce_paged_attention_decode_noalloc(
+    int dtype, const void *query, const void *key_cache, const void *value_cache,
+    const int32_t *block_tables, const int32_t *context_lens, void *output, int batch,
+    int num_heads, int num_kv_heads, int head_dim, int max_blocks_per_seq, int block_size,
+    int64_t num_blocks, float scale, void *stream) {
+  clear_error();
+  const size_t need = mce_paged_attention_decode_workspace_size(
+      batch, num_heads, num_kv_heads, max_blocks_per_seq, block_size);
+  if (need > DECODE_SCRATCH_BYTES)
+    return set_error(MCE_ERR_UNSUPPORTED,
+                     "mce_paged_attention_decode_noalloc: this shape needs %zu bytes of split-K "
+                     "scratch, above the library's static %zu (use mce_paged_attention_decode "
+                     "with a workspace)",
+                     need, DECODE_SCRATCH_BYTES);
+  void *ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_address(&ws);
+    if (rc != MCE_OK) return rc;
+  }
+  return decode_impl(dtype, query, key_cache, value_cache, block_tables, context_lens, output,
+                     batch, num_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size,
+                     num_blocks, scale, ws, need > 0 ? DECODE_SCRATCH_BYTES : 0, stream,
+                     FusedRope{});
 }
 
 extern "C" int mce_paged_attention_decode_rope(

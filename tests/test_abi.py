@@ -19,6 +19,7 @@ HEADER_ENTRY_POINTS = {
     "mce_rope_kv_store", "mce_decode_gemm", "mce_paged_attention_decode_rope",
     "mce_rmsnorm_decode_gemm", "mce_argmax_rows", "mce_decode_advance",
     "mce_prefill_attention_paged", "mce_prefill_attention_paged_workspace_size",
+    "mce_paged_attention_decode_noalloc",
 }
 
 
@@ -120,6 +121,19 @@ def test_decode_workspace_size(lib):
     assert f(16, 32, 32, 128, 16) == expect(16, 32, groups=4)   # 32 kv heads: 4 groups
     if cus == 256:
         assert big < 4 * 2 ** 20                                # 3.6 MB at cfg2
+
+
+def test_decode_noalloc_rejects_shapes_beyond_its_scratch(lib):
+    """The allocation-free decode refuses, before any device work, shapes whose
+    split-K partials would not fit its static scratch (16 MiB)."""
+    f = lib.mce_paged_attention_decode_workspace_size
+    assert _lib.MCE_DECODE_NOALLOC_SCRATCH_BYTES == 16 << 20
+    assert f(2000, 64, 8, 256, 16) > _lib.MCE_DECODE_NOALLOC_SCRATCH_BYTES
+    p = ctypes.c_void_p(16)
+    rc = lib.mce_paged_attention_decode_noalloc(0, p, p, p, p, p, p, 2000, 64, 8, 128, 256, 16,
+                                                 1000, 0.1, None)
+    assert rc == _lib.MCE_ERR_UNSUPPORTED
+    assert b"static" in lib.mce_last_error()
 
 
 def test_rope_and_prefill_validation(lib):
