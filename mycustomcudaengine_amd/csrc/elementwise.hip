@@ -199,6 +199,50 @@ __global__ __launch_bounds__(256) void kv_store_vec_kernel(
   }
 }
 
+// head_dim 128 with 16-byte aligned rows: one workgroup per KVS_TOK tokens.
+// A pass of the 256 threads covers 16 head rows (16 threads x 16 bytes per
+// 256-byte row); the workgroup's rows are (token, K or V, head) in that order,
+// and every thread issues all of its loads before its stores.  32-bit index
+// math throughout (the host checks the ranges).
+constexpr int KVS_TOK = 4;
+constexpr int KVS_MAX_PASS = 8;  // rows per thread: 2 * heads * KVS_TOK / 16
+
+__global__ __launch_bounds__(256) void kv_store_d128_kernel(
+    const uint16_t *__restrict__ key, const uint16_t *__restrict__ value,
+    uint16_t *__restrict__ kc, uint16_t *__restrict__ vc, const int32_t *__restrict__ slots,
+    int num_tokens, int heads, int64_t num_slots, int64_t ks_tok, int64_t ks_head,
+    int64_t vs_tok, int64_t vs_head) {
+  const int p = threadIdx.x & 15, r0 = threadIdx.x >> 4;
+  const int rows = 2 * heads * KVS_TOK;
+  const int t0 = blockIdx.x * KVS_TOK;
+  u32x4 val[KVS_MAX_PASS];
+  int64_t dst[KVS_MAX_PASS];
+#pragma unroll
+  for (int j = 0; j < KVS_MAX_PASS; ++j) {
+    const int r = r0 + 16 * j;
+    dst[j] = -1;
+    val[j] = u32x4{0, 0, 0, 0};
+    if (r >= rows) continue;
+    const int tt = r / (2 * heads), rem = r - tt * 2 * heads;
+    const int t = t0 + tt;
+    if (t >= num_tokens) continue;
+    const bool is_v = rem >= heads;
+    const int h = is_v ? rem - heads : rem;
+    const int64_t sl = slots[t];
+    if (sl < 0 || sl >= num_slots) continue;
+    const uint16_t *src = is_v ? value + t * vs_tok + h * vs_head : key + t * ks_tok + h * ks_head;
+    val[j] = *reinterpret_cast<const u32x4 *>(src + 8 * p);
+    dst[j] = ((sl * heads + h) * 128 + 8 * p) | ((int64_t)is_v << 62);
+  }
+#pragma unroll
+  for (int j = 0; j < KVS_MAX_PASS; ++j) {
+    if (dst[j] < 0) continue;
+    const bool is_v = (dst[j] >> 62) & 1;
+    const int64_t off = dst[j] & ~((int64_t)1 << 62);
+    *reinterpret_cast<u32x4 *>((is_v ? vc : kc) + off) = val[j];
+  }
+}
+
 __global__ __launch_bounds__(256) void kv_store_generic_kernel(
     const uint16_t *__restrict__ key, const uint16_t *__restrict__ value,
     uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
@@ -275,6 +319,124 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(
     float c4[4] = {c[0], c[1], c[2], c[3]};
     float s4[4] = {sn[0], sn[1], sn[2], sn[3]};
     rope_rotate4<T>(p + qd * 4, half, c4, s4, p + qd * 4);
+  }
+}
+
+// head_dim 128 with 16-byte aligned rows: a head row is rotated by 8 lanes,
+// lane l8 taking pairs 8 l8 .. 8 l8 + 7 (one 16-byte load from each half of
+// the row, two 16-byte loads of cos and of sin).  Same rope_pair arithmetic
+// as the kernels above, so the results are bit-identical to them.
+template <class T>
+__device__ inline void rope_rotate8(const uint16_t *p, const float *cr, const float *sr, int l8,
+                                    u32x4 &oa, u32x4 &ob) {
+  const u32x4 a = *reinterpret_cast<const u32x4 *>(p + 8 * l8);
+  const u32x4 b = *reinterpret_cast<const u32x4 *>(p + 64 + 8 * l8);
+  const floatx4 c0 = *reinterpret_cast<const floatx4 *>(cr + 8 * l8);
+  const floatx4 c1 = *reinterpret_cast<const floatx4 *>(cr + 8 * l8 + 4);
+  const floatx4 s0 = *reinterpret_cast<const floatx4 *>(sr + 8 * l8);
+  const floatx4 s1 = *reinterpret_cast<const floatx4 *>(sr + 8 * l8 + 4);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float c_lo = k < 2 ? c0[2 * k] : c1[2 * k - 4], c_hi = k < 2 ? c0[2 * k + 1] : c1[2 * k - 3];
+    const float s_lo = k < 2 ? s0[2 * k] : s1[2 * k - 4], s_hi = k < 2 ? s0[2 * k + 1] : s1[2 * k - 3];
+    float r0a, r1a, r0b, r1b;
+    rope_pair(T::lo(a[k]), T::lo(b[k]), c_lo, s_lo, r0a, r1a);
+    rope_pair(T::hi(a[k]), T::hi(b[k]), c_hi, s_hi, r0b, r1b);
+    oa[k] = pack2<T>(r0a, r0b);
+    ob[k] = pack2<T>(r1a, r1b);
+  }
+}
+
+// the two 16-byte halves of lane l8's piece of a 128-wide row
+__device__ inline void store_row8(uint16_t *dst, int l8, const u32x4 &lo, const u32x4 &hi) {
+  *reinterpret_cast<u32x4 *>(dst + 8 * l8) = lo;
+  *reinterpret_cast<u32x4 *>(dst + 64 + 8 * l8) = hi;
+}
+
+// rope_inplace for head_dim 128: one workgroup per ROPE_TOK tokens, a pass of
+// 256 threads covering 32 head rows (query heads, then key heads, per token).
+constexpr int ROPE_TOK = 2;
+
+template <class T>
+__global__ __launch_bounds__(256) void rope_d128_kernel(
+    uint16_t *__restrict__ q, uint16_t *__restrict__ k, const float *__restrict__ cos_t,
+    const float *__restrict__ sin_t, const int32_t *__restrict__ pos, int tokens, int seq_len,
+    int num_heads, int num_kv_heads, int64_t table_rows, int64_t qsb, int64_t qss, int64_t qsh,
+    int64_t ksb, int64_t kss, int64_t ksh) {
+  const int l8 = threadIdx.x & 7;
+  const int heads = num_heads + num_kv_heads;
+  const int rows = heads * ROPE_TOK;
+  const int t0 = blockIdx.x * ROPE_TOK;
+  for (int r = threadIdx.x >> 3; r < rows; r += 32) {
+    const int tt = r / heads, h = r - tt * heads;
+    const int t = t0 + tt;
+    if (t >= tokens) break;
+    const int64_t ps = pos[t];
+    if (ps < 0 || ps >= table_rows) continue;
+    const int b = t / seq_len, s = t - b * seq_len;
+    uint16_t *p = h < num_heads ? q + b * qsb + s * qss + h * qsh
+                                : k + b * ksb + s * kss + (h - num_heads) * ksh;
+    u32x4 lo, hi;
+    rope_rotate8<T>(p, cos_t + ps * 64, sin_t + ps * 64, l8, lo, hi);
+    store_row8(p, l8, lo, hi);
+  }
+}
+
+// rope_kv_store for head_dim 128: like rope_d128_kernel over the rows
+// (query heads, key heads, value heads) of each token.
+template <class T>
+__global__ __launch_bounds__(256) void rope_kv_store_d128_kernel(
+    uint16_t *__restrict__ q, uint16_t *__restrict__ q_out, uint16_t *__restrict__ k,
+    const uint16_t *__restrict__ v, uint16_t *__restrict__ kc, uint16_t *__restrict__ vc,
+    const float *__restrict__ cos_t, const float *__restrict__ sin_t,
+    const int32_t *__restrict__ pos, const int32_t *__restrict__ slots, int tokens,
+    int num_heads, int num_kv_heads, int64_t table_rows, int64_t num_slots, int64_t qst,
+    int64_t qsh, int64_t kst, int64_t ksh, int64_t vst, int64_t vsh) {
+  const int l8 = threadIdx.x & 7;
+  const int heads = num_heads + 2 * num_kv_heads;
+  const int rows = heads * ROPE_TOK;
+  const int t0 = blockIdx.x * ROPE_TOK;
+  for (int r = threadIdx.x >> 3; r < rows; r += 32) {
+    const int tt = r / heads, h = r - tt * heads;
+    const int t = t0 + tt;
+    if (t >= tokens) break;
+    const int64_t ps = pos[t];
+    const bool in_table = ps >= 0 && ps < table_rows;
+    const float *cr = cos_t + (in_table ? ps : 0) * 64, *sr = sin_t + (in_table ? ps : 0) * 64;
+    if (h < num_heads) {
+      uint16_t *p = q + t * qst + h * qsh;
+      uint16_t *dst = q_out ? q_out + ((int64_t)t * num_heads + h) * 128 : p;
+      if (in_table) {
+        u32x4 lo, hi;
+        rope_rotate8<T>(p, cr, sr, l8, lo, hi);
+        store_row8(dst, l8, lo, hi);
+      } else if (q_out) {
+        store_row8(dst, l8, *reinterpret_cast<const u32x4 *>(p + 8 * l8),
+                   *reinterpret_cast<const u32x4 *>(p + 64 + 8 * l8));
+      }
+      continue;
+    }
+    const int64_t sl = slots[t];
+    const bool store = sl >= 0 && sl < num_slots;
+    if (h < num_heads + num_kv_heads) {
+      const int hk = h - num_heads;
+      uint16_t *p = k + t * kst + hk * ksh;
+      u32x4 lo, hi;
+      if (in_table) {
+        rope_rotate8<T>(p, cr, sr, l8, lo, hi);
+        store_row8(p, l8, lo, hi);
+      } else {
+        lo = *reinterpret_cast<const u32x4 *>(p + 8 * l8);
+        hi = *reinterpret_cast<const u32x4 *>(p + 64 + 8 * l8);
+      }
+      if (store) store_row8(kc + (sl * num_kv_heads + hk) * 128, l8, lo, hi);
+    } else if (store) {
+      const int hv = h - num_heads - num_kv_heads;
+      const uint16_t *p = v + t * vst + hv * vsh;
+      store_row8(vc + (sl * num_kv_heads + hv) * 128, l8,
+                 *reinterpret_cast<const u32x4 *>(p + 8 * l8),
+                 *reinterpret_cast<const u32x4 *>(p + 64 + 8 * l8));
+    }
   }
 }
 
@@ -451,7 +613,13 @@ extern "C" int mce_paged_kv_store(int dtype, const void *key, const void *value,
                    aligned16(value) && aligned16(key_cache) &&
                    aligned16(value_cache);
   const int64_t work = num_tokens * num_kv_heads * (vec ? head_dim / 8 : head_dim);
-  if (vec)
+  if (vec && head_dim == 128 && 2 * num_kv_heads * KVS_TOK <= 16 * KVS_MAX_PASS &&
+      num_tokens < ((int64_t)1 << 31) - KVS_TOK)
+    kv_store_d128_kernel<<<(unsigned)((num_tokens + KVS_TOK - 1) / KVS_TOK), 256, 0, st>>>(
+        (const uint16_t *)key, (const uint16_t *)value, (uint16_t *)key_cache,
+        (uint16_t *)value_cache, slot_mapping, (int)num_tokens, num_kv_heads, num_slots,
+        key_stride_tok, key_stride_head, value_stride_tok, value_stride_head);
+  else if (vec)
     kv_store_vec_kernel<<<grid_for(work), 256, 0, st>>>(
         (const uint16_t *)key, (const uint16_t *)value, (uint16_t *)key_cache,
         (uint16_t *)value_cache, slot_mapping, num_tokens, num_kv_heads,
@@ -496,7 +664,24 @@ extern "C" int mce_rope_inplace(int dtype, void *query, void *key,
           k_stride_h % 4 == 0 && (reinterpret_cast<uintptr_t>(key) & 7) == 0;
   const int heads = num_heads + num_kv_heads;
   uint16_t *q = (uint16_t *)query, *k = (uint16_t *)key;
-  if (vec) {
+  const bool d128 = head_dim == 128 && tokens < ((int64_t)1 << 31) - ROPE_TOK &&
+                    q_stride_b % 8 == 0 && q_stride_s % 8 == 0 && q_stride_h % 8 == 0 &&
+                    aligned16(query) && aligned16(cos_table) && aligned16(sin_table) &&
+                    (!key || (k_stride_b % 8 == 0 && k_stride_s % 8 == 0 &&
+                              k_stride_h % 8 == 0 && aligned16(key)));
+  if (d128) {
+    const unsigned grid = (unsigned)((tokens + ROPE_TOK - 1) / ROPE_TOK);
+    if (dtype == MCE_F16)
+      rope_d128_kernel<F16T><<<grid, 256, 0, st>>>(q, k, cos_table, sin_table, positions,
+                                                   (int)tokens, seq_len, num_heads, num_kv_heads,
+                                                   table_rows, q_stride_b, q_stride_s, q_stride_h,
+                                                   k_stride_b, k_stride_s, k_stride_h);
+    else
+      rope_d128_kernel<BF16T><<<grid, 256, 0, st>>>(q, k, cos_table, sin_table, positions,
+                                                    (int)tokens, seq_len, num_heads, num_kv_heads,
+                                                    table_rows, q_stride_b, q_stride_s, q_stride_h,
+                                                    k_stride_b, k_stride_s, k_stride_h);
+  } else if (vec) {
     const int64_t work = tokens * heads * (half / 4);
     if (dtype == MCE_F16)
       rope_vec_kernel<F16T><<<grid_for(work), 256, 0, st>>>(q, k, cos_table, sin_table, positions, tokens, seq_len, num_heads, num_kv_heads, head_dim, table_rows, q_stride_b, q_stride_s, q_stride_h, k_stride_b, k_stride_s, k_stride_h);
@@ -566,9 +751,29 @@ extern "C" int mce_rope_kv_store(int dtype, void *query, void *query_out, void *
                               num_tokens, num_kv_heads, head_dim, block_size, num_blocks,
                               k_stride_tok, k_stride_head, v_stride_tok, v_stride_head, stream);
   }
-  MCE_REQUIRE(num_tokens < ((int64_t)1 << 31), "mce_rope_kv_store: too many tokens");
+  MCE_REQUIRE(num_tokens < ((int64_t)1 << 31) - ROPE_TOK, "mce_rope_kv_store: too many tokens");
   hipStream_t st = (hipStream_t)stream;
   const int64_t num_slots = num_blocks * block_size;
+  const bool d128 = head_dim == 128 && q_stride_tok % 8 == 0 && q_stride_head % 8 == 0 &&
+                    k_stride_tok % 8 == 0 && k_stride_head % 8 == 0 && v_stride_tok % 8 == 0 &&
+                    v_stride_head % 8 == 0 && aligned16(query) && aligned16(key) &&
+                    aligned16(value) && aligned16(key_cache) && aligned16(value_cache) &&
+                    (!query_out || aligned16(query_out));
+  if (d128) {
+    const unsigned grid = (unsigned)((num_tokens + ROPE_TOK - 1) / ROPE_TOK);
+#define MCE_RKV128(TT)                                                                           \
+  rope_kv_store_d128_kernel<TT><<<grid, 256, 0, st>>>(                                           \
+      (uint16_t *)query, (uint16_t *)query_out, (uint16_t *)key, (const uint16_t *)value,        \
+      (uint16_t *)key_cache, (uint16_t *)value_cache, cos_table, sin_table, positions,           \
+      slot_mapping, (int)num_tokens, num_heads, num_kv_heads, table_rows, num_slots,             \
+      q_stride_tok, q_stride_head, k_stride_tok, k_stride_head, v_stride_tok, v_stride_head)
+    if (dtype == MCE_F16)
+      MCE_RKV128(F16T);
+    else
+      MCE_RKV128(BF16T);
+#undef MCE_RKV128
+    return check_launch("mce_rope_kv_store");
+  }
   const int64_t work = num_tokens * (num_heads + 2 * num_kv_heads) * (half / 4);
 #define MCE_RKV(TT)                                                                              \
   rope_kv_store_vec_kernel<TT><<<grid_for(work), 256, 0, st>>>(                                  \

@@ -165,6 +165,49 @@ def test_kv_store_strided_token_views(dev):
         assert torch.equal(got, torch.from_numpy(vr))
 
 
+def test_rope_and_kv_store_kernels_agree_across_layouts(dev):
+    """16-byte aligned head_dim-128 rows take the workgroup-per-token kernels;
+    the same values in rows offset by 8 bytes take the generic vector
+    kernels: bit-identical results (same rotation arithmetic), and head_dim
+    64 (generic kernels) bit-exact / within the bar against the oracle."""
+    n, hq, hkv = 37, 6, 2
+    cos, sin = rope_tables(128, 128, 500000.0)
+    g = gen(77)
+    q = torch.randn(n, 1, hq, 128, generator=g).half()
+    k = torch.randn(n, 1, hkv, 128, generator=g).half()
+    pos = torch.randint(0, 128, (n, 1), generator=g, dtype=torch.int32).to(dev)
+    outs = []
+    for shift in (0, 4):  # elements: 0 -> 16-byte aligned rows, 4 -> 8-byte aligned
+        qb = torch.zeros(n * hq * 128 + 8, dtype=torch.float16, device=dev)
+        kb = torch.zeros(n * hkv * 128 + 8, dtype=torch.float16, device=dev)
+        qv = qb[shift:shift + n * hq * 128].view(n, 1, hq, 128)
+        kv = kb[shift:shift + n * hkv * 128].view(n, 1, hkv, 128)
+        qv.copy_(q.to(dev))
+        kv.copy_(k.to(dev))
+        ops.rope_inplace(qv, kv, cos.to(dev), sin.to(dev), pos)
+        outs.append((qv.cpu(), kv.cpu()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    # kv store: aligned d128 rows vs 16-byte aligned head_dim 64 (generic kernel)
+    for d in (128, 64):
+        key = torch.randn(n, hkv, d, generator=g).half()
+        val = torch.randn(n, hkv, d, generator=g).half()
+        slots = torch.randperm(40 * 16, generator=g)[:n].to(torch.int32)
+        slots[3] = -1
+        kc = torch.zeros(40, 16, hkv, d).half()
+        vc = torch.zeros(40, 16, hkv, d).half()
+        kcd, vcd = kc.to(dev), vc.to(dev)
+        ops.paged_kv_store(key.to(dev), val.to(dev), kcd, vcd, slots.to(dev))
+        kr, vr = kc.numpy().copy(), vc.numpy().copy()
+        kv_store_ref(key.numpy(), val.numpy(), kr, vr, slots.numpy())
+        assert torch.equal(kcd.cpu(), torch.from_numpy(kr)) and torch.equal(vcd.cpu(), torch.from_numpy(vr))
+    cos64, sin64 = rope_tables(128, 64, 500000.0)
+    q64 = torch.randn(2, 5, 4, 64, generator=g).half()
+    p64 = torch.arange(5, dtype=torch.int32).repeat(2, 1)
+    q64d = q64.to(dev)
+    ops.rope_inplace(q64d, None, cos64.to(dev), sin64.to(dev), p64.to(dev))
+    assert rel_close(q64d.cpu(), rope_ref(q64, cos64, sin64, p64), 4e-3, 2e-3)[0]
+
+
 # ------------------------------------------------------------ causal prefill
 @pytest.mark.parametrize("s", [1, 2, 17, 64, 127, 128, 129, 300, 512, 1000])
 @pytest.mark.parametrize("hq,hkv", [(24, 8), (4, 4), (6, 2)])
