@@ -56,22 +56,27 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_gpu(fn, steps: int, warmup: int) -> float:
+def time_gpu(fn, steps: int, warmup: int, rounds: int = 1) -> float:
     """Average ms per call of fn(), issued eagerly from Python, measured with
-    HIP events on the current stream (includes host launch overhead when the
-    GPU work is shorter than the Python call)."""
+    HIP events on the current stream over `steps` back-to-back calls (includes
+    host launch overhead when the GPU work is shorter than the Python call).
+    rounds > 1: the median of that many such windows (the first windows after
+    other work can run at lower clocks)."""
     for _ in range(warmup):
         fn()
     stream = torch.cuda.current_stream()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(steps):
-        fn()
-    stop.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps
+    times = []
+    for _ in range(rounds):
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(steps):
+            fn()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(stop) / steps)
+    return sorted(times)[len(times) // 2]
 
 
 def time_graph(fn, steps: int, warmup: int) -> float:
@@ -104,7 +109,8 @@ def time_graph(fn, steps: int, warmup: int) -> float:
 
 def time_graph_batch(fn, calls: int = 20, replays: int = 20, warmup: int = 3) -> float:
     """Average ms per call of fn() with `calls` back-to-back calls captured in
-    one hipGraph, replayed `replays` times (HIP events around the replays):
+    one hipGraph, replayed `replays` times (HIP events around the replays;
+    the median of 5 such windows):
     per-kernel time plus the gap between consecutive kernels, without the
     host's per-call Python work (which exceeds a few-microsecond kernel)."""
     s = torch.cuda.Stream()
@@ -121,15 +127,18 @@ def time_graph_batch(fn, calls: int = 20, replays: int = 20, warmup: int = 3) ->
     for _ in range(warmup):
         graph.replay()
     stream = torch.cuda.current_stream()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(replays):
-        graph.replay()
-    stop.record(stream)
-    torch.cuda.synchronize()
-    return start.elapsed_time(stop) / (replays * calls)
+    times = []
+    for _ in range(5):  # median of 5 windows
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(stop) / (replays * calls))
+    return sorted(times)[2]
 
 
 def cpu_info() -> dict:
@@ -145,14 +154,14 @@ def cpu_info() -> dict:
     return {"cpu_model": model, "torch": torch.__version__}
 
 
-def bench_decode(case, dev, steps, warmup):
+def bench_decode(case, dev, steps, warmup, rounds=1):
     import my_cuda_engine_cpp as ops
     q = case.query.to(dev)
     kc, vc = case.key_cache.to(dev), case.value_cache.to(dev)
     bt, cl = case.block_tables.to(dev), case.context_lens.to(dev)
     fn = lambda: ops.paged_attention_decode(q, kc, vc, bt, cl, case.max_blocks,
                                             case.block_size, case.scale)
-    ms = time_gpu(fn, steps, warmup)
+    ms = time_gpu(fn, steps, warmup, rounds)
     graph_ms = time_graph(fn, steps, warmup)
     nbytes = case.algorithmic_bytes()
     return ms, nbytes, nbytes / (ms * 1e-3) / 1e9, graph_ms
@@ -164,7 +173,7 @@ def bench_prefill(case, dev, steps, warmup):
     import my_cuda_engine_cpp as ops
     q, k, v = case.query.to(dev), case.key.to(dev), case.value.to(dev)
     fn = lambda: ops.prefill_attention(q, k, v, case.scale)
-    ms = time_gpu(fn, steps, warmup)
+    ms = time_gpu(fn, steps, warmup, rounds=5)
     graph_ms = time_graph(fn, steps, warmup)
     flops = case.algorithmic_flops()
     return ms, flops, flops / (ms * 1e-3) / 1e12, graph_ms
@@ -212,7 +221,7 @@ def bench_prefill_legs(case, dev, steps, warmup) -> dict:
                                                     v.view(s, hkv, d), kc, vc, cos, sin,
                                                     pos.view(-1), slots), fused_b)):
         ms = time_graph_batch(fn)
-        eager_ms = time_gpu(fn, steps, warmup)
+        eager_ms = time_gpu(fn, steps, warmup, rounds=5)
         out[name] = {"us": round(ms * 1e3, 2), "bytes": int(nbytes),
                      "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
                      "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -245,7 +254,7 @@ def bench_harness(dev, steps: int, warmup: int) -> dict:
     scale = d ** -0.5
     nbytes = 2 * b * ctx * h * d * 2 + 2 * b * h * d * 2
     ms = time_gpu(lambda: ops.paged_attention_decode(q, kc, vc, bt, cl, ctx // bs, bs, scale),
-                  steps, warmup)
+                  steps, warmup, rounds=5)
     out = {"workload": "reference decode harness: B=16, 32/32 heads, D=128, ctx 2048, "
                        "ascending tables, fp16",
            "us": round(ms * 1e3, 2), "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
@@ -258,7 +267,7 @@ def bench_harness(dev, steps: int, warmup: int) -> dict:
         # fused backends only (no math fallback through batched GEMMs)
         with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
             sms = time_gpu(lambda: torch.nn.functional.scaled_dot_product_attention(
-                q4, k, v, scale=scale), steps, warmup)
+                q4, k, v, scale=scale), steps, warmup, rounds=5)
         out["sdpa_us"] = round(sms * 1e3, 2)
         out["sdpa_gbs"] = round(nbytes / (sms * 1e-3) / 1e9, 1)
         out["speedup_vs_sdpa"] = round(sms / ms, 3)
@@ -293,7 +302,8 @@ def bench_chunked(dev, steps: int, warmup: int) -> dict:
         row = {}
         for split in (True, False):
             ms = time_gpu(lambda: prefill_attention_paged(q, kc, vc, table, cl, d ** -0.5,
-                                                          split_keys=split), steps, warmup)
+                                                          split_keys=split), steps, warmup,
+                          rounds=5)
             row["split" if split else "whole"] = {"us": round(ms * 1e3, 2),
                                                   "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
         key = f"B{b}_prefix{prefix}_chunk{s}"
@@ -540,7 +550,7 @@ def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["decode", "prefill", "legs", "splitk", "harness", "model",
                                        "chunked"],
@@ -604,7 +614,7 @@ def main() -> None:
     if args.only in (None, "splitk"):
         log("generating cfg4 inputs")
         case4 = cfg4_decode()
-        kms, kbytes, kgbs, _ = bench_decode(case4, dev, max(20, args.steps // 4), 5)
+        kms, kbytes, kgbs, _ = bench_decode(case4, dev, max(20, args.steps // 4), 5, rounds=5)
         log(f"cfg4 split-K decode: {kms * 1e3:.1f} us, {kgbs:.1f} GB/s")
         extra["splitk"] = {"workload": "cfg4 paged decode B=8 ctx=32768 24/8 heads D=128",
                            "us": round(kms * 1e3, 2), "bytes": kbytes,

@@ -37,23 +37,28 @@ __all__ = [
 _DTYPES = {torch.float16: _lib.MCE_F16, torch.bfloat16: _lib.MCE_BF16}
 
 
-def _check(cond: bool, msg: str) -> None:
+def _check(cond: bool, msg) -> None:
+    """Raises RuntimeError(msg) when cond is false; msg may be a callable that
+    builds the message (formatted only on failure: these checks run on every
+    op call)."""
     if not cond:
-        raise RuntimeError(msg)
+        raise RuntimeError(msg() if callable(msg) else msg)
 
 
 def _dtype_code(t: torch.Tensor, name: str) -> int:
     code = _DTYPES.get(t.dtype)
-    _check(code is not None, f"{name} must be float16 or bfloat16 (got {t.dtype})")
+    _check(code is not None,
+           lambda: f"{name() if callable(name) else name} must be float16 or bfloat16 "
+                   f"(got {t.dtype})")
     return code
 
 
 def _on_gpu(name: str, *ts: torch.Tensor) -> torch.device:
     dev = ts[0].device
     for t in ts:
-        _check(isinstance(t, torch.Tensor), f"{name}: expected tensors")
-        _check(t.is_cuda, f"{name}: tensors must be on a GPU (got {t.device})")
-        _check(t.device == dev, f"{name}: tensors are on different devices")
+        _check(isinstance(t, torch.Tensor), lambda: f"{name}: expected tensors")
+        _check(t.is_cuda, lambda: f"{name}: tensors must be on a GPU (got {t.device})")
+        _check(t.device == dev, lambda: f"{name}: tensors are on different devices")
     return dev
 
 
@@ -87,7 +92,7 @@ def rmsnorm(input: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tens
     _check(input.dim() >= 1, "rmsnorm: input must have at least one dim")
     hidden = input.size(-1)
     _check(weight.dim() == 1 and weight.size(0) == hidden and weight.is_contiguous(),
-           f"rmsnorm: weight must be contiguous [{hidden}]")
+           lambda: f"rmsnorm: weight must be contiguous [{hidden}]")
     x = input if input.is_contiguous() else input.contiguous()
     out = torch.empty_like(x)
     rows = x.numel() // hidden if hidden else 0
@@ -103,7 +108,7 @@ def swiglu(gate_up: torch.Tensor) -> torch.Tensor:
     code = _dtype_code(gate_up, "swiglu gate_up")
     _check(gate_up.dim() >= 1, "swiglu: input must have at least one dim")
     two_i = gate_up.size(-1)
-    _check(two_i % 2 == 0, f"swiglu: last dim must be even (got {two_i})")
+    _check(two_i % 2 == 0, lambda: f"swiglu: last dim must be even (got {two_i})")
     x = gate_up if gate_up.is_contiguous() else gate_up.contiguous()
     inter = two_i // 2
     shape = list(x.shape)
@@ -126,28 +131,42 @@ def paged_kv_store(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tens
     dev = _on_gpu("paged_kv_store", key, value, key_cache, value_cache, slot_mapping)
     code = _dtype_code(key, "paged_kv_store key")
     for t, n in ((value, "value"), (key_cache, "key_cache"), (value_cache, "value_cache")):
-        _check(t.dtype == key.dtype, f"paged_kv_store: {n} dtype must match key")
+        _check(t.dtype == key.dtype, lambda: f"paged_kv_store: {n} dtype must match key")
     _check(key.dim() == 3 and value.shape == key.shape,
-           f"paged_kv_store: key/value must be [N, Hkv, D] (got {tuple(key.shape)}, "
+           lambda: f"paged_kv_store: key/value must be [N, Hkv, D] (got {tuple(key.shape)}, "
            f"{tuple(value.shape)})")
     n_tok, hkv, d = key.shape
     _check(key_cache.dim() == 4 and key_cache.shape == value_cache.shape,
            "paged_kv_store: caches must be [num_blocks, block_size, Hkv, D]")
     nb, bs, chkv, cd = key_cache.shape
     _check(chkv == hkv and cd == d,
-           f"paged_kv_store: cache head shape {(chkv, cd)} != key head shape {(hkv, d)}")
+           lambda: f"paged_kv_store: cache head shape {(chkv, cd)} != key head shape {(hkv, d)}")
     _check(key_cache.is_contiguous() and value_cache.is_contiguous(),
            "paged_kv_store: caches must be contiguous")
     _check(key.stride(-1) == 1 and value.stride(-1) == 1,
            "paged_kv_store: key/value last dim must be contiguous")
     _check(slot_mapping.dtype == torch.int32 and slot_mapping.dim() == 1 and
            slot_mapping.size(0) == n_tok and slot_mapping.is_contiguous(),
-           f"paged_kv_store: slot_mapping must be contiguous int32 [{n_tok}]")
+           lambda: f"paged_kv_store: slot_mapping must be contiguous int32 [{n_tok}]")
     with _on_device(dev):
         _lib.call("mce_paged_kv_store", code, key.data_ptr(), value.data_ptr(),
                   key_cache.data_ptr(), value_cache.data_ptr(), slot_mapping.data_ptr(),
                   n_tok, hkv, d, bs, nb, key.stride(0), key.stride(1),
                   value.stride(0), value.stride(1), _stream(dev))
+
+
+_DECODE_WS = {}  # (device, batch, heads, kv heads, table width, block size) -> bytes
+
+
+def _decode_workspace_bytes(device: int, b: int, hq: int, hkv: int, mb: int, bs: int) -> int:
+    """mce_paged_attention_decode_workspace_size for the current device, cached
+    per shape (the size depends on the device's CU count and the shape only)."""
+    key = (device, b, hq, hkv, mb, bs)
+    size = _DECODE_WS.get(key)
+    if size is None:
+        size = _DECODE_WS[key] = _lib.load().mce_paged_attention_decode_workspace_size(
+            b, hq, hkv, mb, bs)
+    return size
 
 
 def paged_attention_decode(query: torch.Tensor, key_cache: torch.Tensor,
@@ -170,25 +189,24 @@ def paged_attention_decode(query: torch.Tensor, key_cache: torch.Tensor,
     _check(key_cache.dim() == 4 and key_cache.shape == value_cache.shape,
            "paged_attention_decode: caches must be [num_blocks, block_size, Hkv, D]")
     nb, bs, hkv, cd = key_cache.shape
-    _check(cd == d, f"paged_attention_decode: cache head_dim {cd} != query head_dim {d}")
+    _check(cd == d, lambda: f"paged_attention_decode: cache head_dim {cd} != query head_dim {d}")
     _check(int(block_size) == bs,
-           f"paged_attention_decode: block_size {block_size} != cache block size {bs}")
+           lambda: f"paged_attention_decode: block_size {block_size} != cache block size {bs}")
     _check(key_cache.is_contiguous() and value_cache.is_contiguous(),
            "paged_attention_decode: caches must be contiguous")
     mb = int(max_blocks_per_seq)
     _check(block_tables.dtype == torch.int32 and block_tables.dim() == 2 and
            block_tables.size(0) == b and block_tables.size(1) == mb and
            block_tables.is_contiguous(),
-           f"paged_attention_decode: block_tables must be contiguous int32 [{b}, {mb}] "
+           lambda: f"paged_attention_decode: block_tables must be contiguous int32 [{b}, {mb}] "
            f"(got {block_tables.dtype} {tuple(block_tables.shape)})")
     _check(context_lens.dtype == torch.int32 and context_lens.dim() == 1 and
            context_lens.size(0) == b and context_lens.is_contiguous(),
-           f"paged_attention_decode: context_lens must be contiguous int32 [{b}]")
+           lambda: f"paged_attention_decode: context_lens must be contiguous int32 [{b}]")
     q = query if query.is_contiguous() else query.contiguous()
     out = torch.empty_like(q)
     with _on_device(dev):
-        lib = _lib.load()
-        ws_bytes = lib.mce_paged_attention_decode_workspace_size(b, hq, hkv, mb, bs) if b else 0
+        ws_bytes = _decode_workspace_bytes(dev.index, b, hq, hkv, mb, bs) if b else 0
         ws = torch.empty(ws_bytes + 256, dtype=torch.uint8, device=dev) if ws_bytes else None
         ws_ptr = (ws.data_ptr() + 255) & ~255 if ws is not None else None
         _lib.call("mce_paged_attention_decode", code, q.data_ptr(), key_cache.data_ptr(),
@@ -210,22 +228,22 @@ def rope_inplace(query: torch.Tensor, key, cos_table: torch.Tensor,
     code = _dtype_code(query, "rope_inplace query")
     _check(query.dim() == 4, "rope_inplace: query must be [B, S, Hq, D]")
     b, s, hq, d = query.shape
-    _check(d % 2 == 0, f"rope_inplace: head_dim must be even (got {d})")
+    _check(d % 2 == 0, lambda: f"rope_inplace: head_dim must be even (got {d})")
     _check(query.stride(-1) == 1, "rope_inplace: query last dim must be contiguous")
     hkv = 0
     if key is not None:
         _check(key.dtype == query.dtype, "rope_inplace: key dtype must match query")
         _check(key.dim() == 4 and key.size(0) == b and key.size(1) == s and key.size(3) == d,
-               f"rope_inplace: key must be [{b}, {s}, Hkv, {d}] (got {tuple(key.shape)})")
+               lambda: f"rope_inplace: key must be [{b}, {s}, Hkv, {d}] (got {tuple(key.shape)})")
         _check(key.stride(-1) == 1, "rope_inplace: key last dim must be contiguous")
         hkv = key.size(2)
     for t, n in ((cos_table, "cos_table"), (sin_table, "sin_table")):
         _check(t.dtype == torch.float32 and t.dim() == 2 and t.size(1) == d // 2 and
-               t.is_contiguous(), f"rope_inplace: {n} must be contiguous fp32 [P, {d // 2}]")
+               t.is_contiguous(), lambda: f"rope_inplace: {n} must be contiguous fp32 [P, {d // 2}]")
     _check(cos_table.size(0) == sin_table.size(0), "rope_inplace: table lengths differ")
     _check(positions.dtype == torch.int32 and positions.numel() == b * s and
            positions.is_contiguous(),
-           f"rope_inplace: positions must be contiguous int32 with {b * s} elements")
+           lambda: f"rope_inplace: positions must be contiguous int32 with {b * s} elements")
     ks = key.stride() if key is not None else (0, 0, 0, 0)
     with _on_device(dev):
         _lib.call("mce_rope_inplace", code, query.data_ptr(),
@@ -254,15 +272,15 @@ def rope_kv_store(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     code = _dtype_code(query, "rope_kv_store query")
     for t, n in ((key, "key"), (value, "value"), (key_cache, "key_cache"),
                  (value_cache, "value_cache")):
-        _check(t.dtype == query.dtype, f"rope_kv_store: {n} dtype must match query")
+        _check(t.dtype == query.dtype, lambda: f"rope_kv_store: {n} dtype must match query")
     _check(query.dim() == 3 and key.dim() == 3 and value.shape == key.shape and
            key.size(0) == query.size(0) and key.size(2) == query.size(2),
            "rope_kv_store: query [N, Hq, D], key/value [N, Hkv, D] expected")
     n_tok, hq, d = query.shape
     hkv = key.size(1)
-    _check(d % 2 == 0, f"rope_kv_store: head_dim must be even (got {d})")
+    _check(d % 2 == 0, lambda: f"rope_kv_store: head_dim must be even (got {d})")
     for t, n in ((query, "query"), (key, "key"), (value, "value")):
-        _check(t.stride(-1) == 1, f"rope_kv_store: {n} last dim must be contiguous")
+        _check(t.stride(-1) == 1, lambda: f"rope_kv_store: {n} last dim must be contiguous")
     _check(key_cache.dim() == 4 and key_cache.shape == value_cache.shape and
            key_cache.size(2) == hkv and key_cache.size(3) == d and
            key_cache.is_contiguous() and value_cache.is_contiguous(),
@@ -270,11 +288,11 @@ def rope_kv_store(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     nb, bs = key_cache.shape[:2]
     for t, n in ((cos_table, "cos_table"), (sin_table, "sin_table")):
         _check(t.dtype == torch.float32 and t.dim() == 2 and t.size(1) == d // 2 and
-               t.is_contiguous(), f"rope_kv_store: {n} must be contiguous fp32 [P, {d // 2}]")
+               t.is_contiguous(), lambda: f"rope_kv_store: {n} must be contiguous fp32 [P, {d // 2}]")
     _check(cos_table.size(0) == sin_table.size(0), "rope_kv_store: table lengths differ")
     for t, n in ((positions, "positions"), (slot_mapping, "slot_mapping")):
         _check(t.dtype == torch.int32 and t.numel() == n_tok and t.is_contiguous(),
-               f"rope_kv_store: {n} must be contiguous int32 with {n_tok} elements")
+               lambda: f"rope_kv_store: {n} must be contiguous int32 with {n_tok} elements")
     if query_out is not None:
         _check(query_out.dtype == query.dtype and query_out.shape == query.shape and
                query_out.is_contiguous() and query_out.device == query.device,
@@ -311,7 +329,7 @@ def decode_rope_attention(query: torch.Tensor, key: torch.Tensor, value: torch.T
     code = _dtype_code(query, "decode_rope_attention query")
     for t, n in ((key, "key"), (value, "value"), (key_cache, "key_cache"),
                  (value_cache, "value_cache")):
-        _check(t.dtype == query.dtype, f"decode_rope_attention: {n} dtype must match query")
+        _check(t.dtype == query.dtype, lambda: f"decode_rope_attention: {n} dtype must match query")
     _check(query.dim() == 3 and key.dim() == 3 and value.shape == key.shape and
            key.size(0) == query.size(0) and key.size(2) == query.size(2),
            "decode_rope_attention: query [B, Hq, D], key/value [B, Hkv, D] expected")
@@ -319,7 +337,7 @@ def decode_rope_attention(query: torch.Tensor, key: torch.Tensor, value: torch.T
     hkv = key.size(1)
     for t, n in ((query, "query"), (key, "key"), (value, "value")):
         _check(t.stride(2) == 1 and t.stride(1) == d,
-               f"decode_rope_attention: {n} heads must be contiguous rows of head_dim")
+               lambda: f"decode_rope_attention: {n} heads must be contiguous rows of head_dim")
     _check(key.stride(0) == value.stride(0),
            "decode_rope_attention: key and value need the same batch stride")
     _check(key_cache.dim() == 4 and key_cache.shape == value_cache.shape and
@@ -329,21 +347,21 @@ def decode_rope_attention(query: torch.Tensor, key: torch.Tensor, value: torch.T
     nb, bs = key_cache.shape[:2]
     mb = int(max_blocks_per_seq)
     _check(mb * bs <= PER_SEQ_MAX_TOKENS,
-           f"decode_rope_attention: table capacity {mb * bs} > {PER_SEQ_MAX_TOKENS}; use "
+           lambda: f"decode_rope_attention: table capacity {mb * bs} > {PER_SEQ_MAX_TOKENS}; use "
            "rope_kv_store + paged_attention_decode")
     for t, n in ((cos_table, "cos_table"), (sin_table, "sin_table")):
         _check(t.dtype == torch.float32 and t.dim() == 2 and t.size(1) == d // 2 and
-               t.is_contiguous(), f"decode_rope_attention: {n} must be contiguous fp32 "
+               t.is_contiguous(), lambda: f"decode_rope_attention: {n} must be contiguous fp32 "
                f"[P, {d // 2}]")
     _check(cos_table.size(0) == sin_table.size(0), "decode_rope_attention: table lengths differ")
     for t, n in ((positions, "positions"), (slot_mapping, "slot_mapping"),
                  (context_lens, "context_lens")):
         _check(t.dtype == torch.int32 and t.numel() == b and t.is_contiguous(),
-               f"decode_rope_attention: {n} must be contiguous int32 with {b} elements")
+               lambda: f"decode_rope_attention: {n} must be contiguous int32 with {b} elements")
     _check(block_tables.dtype == torch.int32 and block_tables.dim() == 2 and
            block_tables.size(0) == b and block_tables.size(1) == mb and
            block_tables.is_contiguous(),
-           f"decode_rope_attention: block_tables must be contiguous int32 [{b}, {mb}]")
+           lambda: f"decode_rope_attention: block_tables must be contiguous int32 [{b}, {mb}]")
     out = torch.empty(b, hq, d, dtype=query.dtype, device=query.device)
     with _on_device(dev):
         _lib.call("mce_paged_attention_decode_rope", code, query.data_ptr(), key.data_ptr(),
@@ -362,24 +380,24 @@ def _projection(name: str, x: torch.Tensor, weight: torch.Tensor, out, epilogue:
     """Shared argument checks of the decode-sized projections; returns
     (device, dtype code, m, n, k, out)."""
     dev = _on_gpu(name, x, weight)
-    code = _dtype_code(x, f"{name} x")
-    _check(weight.dtype == x.dtype, f"{name}: weight dtype must match x")
+    code = _dtype_code(x, lambda: f"{name} x")
+    _check(weight.dtype == x.dtype, lambda: f"{name}: weight dtype must match x")
     _check(x.dim() == 2 and weight.dim() == 2 and x.size(1) == weight.size(1),
-           f"{name}: x [M, K] and weight [N, K] expected (got {tuple(x.shape)}, "
+           lambda: f"{name}: x [M, K] and weight [N, K] expected (got {tuple(x.shape)}, "
            f"{tuple(weight.shape)})")
-    _check(epilogue in _EPILOGUES, f"{name}: unknown epilogue {epilogue!r}")
+    _check(epilogue in _EPILOGUES, lambda: f"{name}: unknown epilogue {epilogue!r}")
     _check(x.stride(1) == 1 and weight.is_contiguous(),
-           f"{name}: x last dim and weight must be contiguous")
+           lambda: f"{name}: x last dim and weight must be contiguous")
     m, k = x.shape
     n = weight.size(0) // 2 if epilogue == "swiglu" else weight.size(0)
     _check(epilogue != "swiglu" or weight.size(0) % 2 == 0,
-           f"{name}: swiglu weight needs an even number of rows")
+           lambda: f"{name}: swiglu weight needs an even number of rows")
     if out is None:
-        _check(epilogue != "add", f"{name}: epilogue 'add' needs out")
+        _check(epilogue != "add", lambda: f"{name}: epilogue 'add' needs out")
         out = torch.empty(m, n, dtype=x.dtype, device=x.device)
     _check(out.dtype == x.dtype and out.dim() == 2 and tuple(out.shape) == (m, n) and
            out.stride(1) == 1 and out.device == x.device,
-           f"{name}: out must be [{m}, {n}] with a contiguous last dim")
+           lambda: f"{name}: out must be [{m}, {n}] with a contiguous last dim")
     return dev, code, m, n, k, out
 
 
@@ -414,7 +432,7 @@ def rmsnorm_decode_gemm(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     dev, code, m, n, k, out = _projection("rmsnorm_decode_gemm", x, weight, out, epilogue)
     _check(norm_weight.device == x.device and norm_weight.dtype == x.dtype and
            norm_weight.dim() == 1 and norm_weight.numel() == k and norm_weight.is_contiguous(),
-           f"rmsnorm_decode_gemm: norm_weight must be a contiguous [{k}] tensor like x")
+           lambda: f"rmsnorm_decode_gemm: norm_weight must be a contiguous [{k}] tensor like x")
     with _on_device(dev):
         _lib.call("mce_rmsnorm_decode_gemm", code, x.data_ptr(), norm_weight.data_ptr(),
                   float(eps), weight.data_ptr(), out.data_ptr(), m, n, k, x.stride(0),
@@ -436,7 +454,7 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
     if out is None:
         out = torch.empty(r, dtype=torch.int64, device=logits.device)
     _check(out.dtype == torch.int64 and out.numel() == r and out.is_contiguous() and
-           out.device == logits.device, f"argmax_rows: out must be {r} contiguous int64 values")
+           out.device == logits.device, lambda: f"argmax_rows: out must be {r} contiguous int64 values")
     with _on_device(dev):
         _lib.call("mce_argmax_rows", code, logits.data_ptr(), r, logits.size(1), logits.stride(0),
                   out.data_ptr(), _stream(dev))
@@ -462,7 +480,7 @@ def decode_advance(block_tables: torch.Tensor, positions: torch.Tensor,
     for name, t in (("positions", positions), ("context_lens", context_lens),
                     ("slot_mapping", slot_mapping)):
         _check(t.dtype == torch.int32 and t.numel() == b and t.is_contiguous() and t.device == dev,
-               f"decode_advance: {name} must be {b} contiguous int32 values")
+               lambda: f"decode_advance: {name} must be {b} contiguous int32 values")
     log_ptr = ids_ptr = ctr_ptr = 0
     cap = 0
     if token_log is not None:
@@ -470,10 +488,10 @@ def decode_advance(block_tables: torch.Tensor, positions: torch.Tensor,
                "decode_advance: token_log needs input_ids and step_counter")
         _check(token_log.dtype == torch.int64 and token_log.dim() == 2 and token_log.size(1) == b
                and token_log.is_contiguous() and token_log.device == dev,
-               f"decode_advance: token_log must be contiguous int64 [steps, {b}]")
+               lambda: f"decode_advance: token_log must be contiguous int64 [steps, {b}]")
         _check(input_ids.dtype == torch.int64 and input_ids.numel() == b and
                input_ids.is_contiguous() and input_ids.device == dev,
-               f"decode_advance: input_ids must be {b} contiguous int64 values")
+               lambda: f"decode_advance: input_ids must be {b} contiguous int64 values")
         _check(step_counter.dtype == torch.int32 and step_counter.numel() >= 1 and
                step_counter.device == dev, "decode_advance: step_counter must be int32")
         log_ptr, ids_ptr, ctr_ptr = token_log.data_ptr(), input_ids.data_ptr(), step_counter.data_ptr()
@@ -498,7 +516,7 @@ def prefill_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tenso
            "prefill_attention: expected query [B, S, Hq, D], key/value [B, S, Hkv, D]")
     b, s, hq, d = query.shape
     _check(key.size(0) == b and key.size(1) == s and key.size(3) == d,
-           f"prefill_attention: key shape {tuple(key.shape)} does not match query "
+           lambda: f"prefill_attention: key shape {tuple(key.shape)} does not match query "
            f"{tuple(query.shape)}")
     hkv = key.size(2)
     q = query if query.is_contiguous() else query.contiguous()
@@ -545,10 +563,10 @@ def prefill_attention_paged(query: torch.Tensor, key_cache: torch.Tensor,
     _check(dk == d, "prefill_attention_paged: head_dim of query and caches differ")
     _check(block_tables.dtype == torch.int32 and block_tables.dim() == 2 and
            block_tables.size(0) == b and block_tables.is_contiguous(),
-           f"prefill_attention_paged: block_tables must be contiguous int32 [{b}, W]")
+           lambda: f"prefill_attention_paged: block_tables must be contiguous int32 [{b}, W]")
     _check(context_lens.dtype == torch.int32 and context_lens.numel() == b and
            context_lens.is_contiguous(),
-           f"prefill_attention_paged: context_lens must be {b} contiguous int32 values")
+           lambda: f"prefill_attention_paged: context_lens must be {b} contiguous int32 values")
     q = query if query.is_contiguous() else query.contiguous()
     out = torch.empty_like(q)
     with _on_device(dev):
