@@ -273,10 +273,19 @@ MCE_API int mce_rmsnorm_decode_gemm(int dtype, const void *x, const void *norm_w
  * number and the lower index wins among equals, as torch.argmax does).
  * Replaces the host-side torch.argmax between replays of the reference's
  * decode loop (benchmarks/benchmark_engine.py:255-265), so the next input
- * ids stay on the device inside a captured graph.
+ * ids stay on the device inside a captured graph.  16-byte aligned rows with a
+ * row stride that is a multiple of 8 are split over up to 64 workgroups each
+ * (4096 columns per part), whose partial maxima go through `workspace` (8-byte
+ * aligned, mce_argmax_rows_workspace_size() bytes, no initialisation; calls
+ * that run concurrently need separate workspaces) to a second, reducing
+ * launch; other rows take one workgroup each and no workspace (NULL allowed).
  */
+/* Workspace bytes mce_argmax_rows needs: rows x parts x 8 (0 for an empty batch). */
+MCE_API size_t mce_argmax_rows_workspace_size(int64_t rows, int64_t cols);
+
 MCE_API int mce_argmax_rows(int dtype, const void *logits, int64_t rows, int64_t cols,
-                            int64_t row_stride, int64_t *out, void *stream);
+                            int64_t row_stride, int64_t *out, void *workspace,
+                            size_t workspace_bytes, void *stream);
 
 /*
  * Prepares the next decode step on the device (one launch, capturable):

@@ -56,7 +56,8 @@ SIGNATURES = {
                                  _c_int, _vp]),
     "mce_rmsnorm_decode_gemm": (_c_int, [_c_int, _vp, _vp, _c_f, _vp, _vp, _c_int, _c_int, _c_int,
                                          _c_i64, _c_i64, _c_int, _vp]),
-    "mce_argmax_rows": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp]),
+    "mce_argmax_rows_workspace_size": (_c_sz, [_c_i64, _c_i64]),
+    "mce_argmax_rows": (_c_int, [_c_int, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_sz, _vp]),
     "mce_prefill_attention_paged_workspace_size": (_c_sz, [_c_int, _c_int, _c_int, _c_int]),
     "mce_prefill_attention_paged": (_c_int, [_c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_int,
                                              _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,

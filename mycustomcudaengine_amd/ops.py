@@ -456,8 +456,12 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor = None) -> torch.Tensor:
     _check(out.dtype == torch.int64 and out.numel() == r and out.is_contiguous() and
            out.device == logits.device, lambda: f"argmax_rows: out must be {r} contiguous int64 values")
     with _on_device(dev):
+        # partial maxima of each row's slices (graph-safe: from torch's allocator)
+        ws_bytes = _lib.load().mce_argmax_rows_workspace_size(r, logits.size(1)) if r else 0
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
         _lib.call("mce_argmax_rows", code, logits.data_ptr(), r, logits.size(1), logits.stride(0),
-                  out.data_ptr(), _stream(dev))
+                  out.data_ptr(), ws.data_ptr() if ws is not None else None, ws_bytes,
+                  _stream(dev))
     return out
 
 

@@ -17,7 +17,8 @@ HEADER_ENTRY_POINTS = {
     "mce_paged_kv_store", "mce_paged_attention_decode_workspace_size",
     "mce_paged_attention_decode", "mce_rope_inplace", "mce_prefill_attention",
     "mce_rope_kv_store", "mce_decode_gemm", "mce_paged_attention_decode_rope",
-    "mce_rmsnorm_decode_gemm", "mce_argmax_rows", "mce_decode_advance",
+    "mce_rmsnorm_decode_gemm", "mce_argmax_rows", "mce_argmax_rows_workspace_size",
+    "mce_decode_advance",
     "mce_prefill_attention_paged", "mce_prefill_attention_paged_workspace_size",
     "mce_paged_attention_decode_noalloc",
 }
@@ -222,11 +223,17 @@ def test_error_exception_carries_status(lib):
 
 def test_decode_loop_entry_points_validate(lib):
     f = lib.mce_argmax_rows
-    assert f(0, None, 8, 100, 100, None, None) == _lib.MCE_ERR_INVALID
+    assert f(0, None, 8, 100, 100, None, None, 0, None) == _lib.MCE_ERR_INVALID
     assert "null" in _err(lib)
-    assert f(0, None, 8, 100, 50, None, None) == _lib.MCE_ERR_INVALID   # stride < cols
-    assert f(2, None, 8, 100, 100, None, None) == _lib.MCE_ERR_INVALID  # dtype
-    assert f(0, None, 0, 100, 100, None, None) == _lib.MCE_OK
+    assert f(0, None, 8, 100, 50, None, None, 0, None) == _lib.MCE_ERR_INVALID   # stride < cols
+    assert f(2, None, 8, 100, 100, None, None, 0, None) == _lib.MCE_ERR_INVALID  # dtype
+    assert f(0, None, 0, 100, 100, None, None, 0, None) == _lib.MCE_OK
+    one = ctypes.c_void_p(16)  # non-null, never dereferenced: validation fails first
+    ws = lib.mce_argmax_rows_workspace_size
+    assert ws(8, 128256) == 8 * 32 * 8 and ws(3, 7) == 3 * 8 and ws(0, 9) == 0
+    # aligned rows are split: the workspace is required
+    assert f(0, one, 8, 128256, 128256, one, None, 0, None) == _lib.MCE_ERR_WORKSPACE
+    assert f(0, one, 8, 128256, 128256, one, one, 8, None) == _lib.MCE_ERR_WORKSPACE
     g = lib.mce_decode_advance
     assert g(None, None, None, None, None, None, None, 4, 8, 16, 0, None) == _lib.MCE_ERR_INVALID
     one = ctypes.c_void_p(16)  # non-null, never dereferenced: validation fails first
