@@ -59,11 +59,15 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g / (1.0f + __expf(-g)) * u;
 }
 
-// EPI: 0 store, 1 add, 2 SwiGLU; TT tiles per workgroup (2 for SwiGLU);
-// MP token slots (8 or 16); NORM: fuse RMSNorm; C chunks of 32 k per wave.
-template <int EPI, int TT, int MP, bool NORM, int C, int WPE>
+// EPI: 0 store, 1 add, 2 SwiGLU; TT tiles per workgroup (SwiGLU: the gate
+// and up tiles); MP token slots (8 or 16); NORM: fuse RMSNorm; C chunks of 32
+// k per wave; R output columns per tile (16, 12, 10 or 8: lanes of rows >= R
+// re-read row R - 1 and their results are dropped), so that the grid can be
+// sized to a whole number of workgroups per CU.
+template <int EPI, int TT, int MP, bool NORM, int C, int WPE, int R>
 __global__ __launch_bounds__(DG_WAVES * 64) __attribute__((amdgpu_waves_per_eu(WPE, WPE)))
 void decode_gemm_kernel(DecodeGemmArgs a) {
+  static_assert(R % 2 == 0 && R >= 8 && R <= 16, "tile rows");
   constexpr int K = C * 256;
   constexpr int VPT = K / 512;      // 16-byte groups of one token row per lane
   constexpr int NTOK = MP / 8;      // token rows staged per wave
@@ -77,7 +81,8 @@ void decode_gemm_kernel(DecodeGemmArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col0 = blockIdx.x * 16;
+  // first output column of the workgroup (SwiGLU: of its gate / up tile pair)
+  const int col0 = blockIdx.x * (EPI == 2 ? R : R * TT);
   const int r = lane & 15, q = lane >> 4;
 
   // 1. this wave's token rows of x (and the norm weights)
@@ -103,7 +108,8 @@ void decode_gemm_kernel(DecodeGemmArgs a) {
   const uint16_t *wp[TT];
 #pragma unroll
   for (int t = 0; t < TT; ++t)
-    wp[t] = a.w + (int64_t)(col0 + t * a.N + r) * K + wave * (K / 8) + 8 * q;
+    wp[t] = a.w + (int64_t)(col0 + t * (EPI == 2 ? a.N : R) + (r < R ? r : R - 1)) * K +
+            wave * (K / 8) + 8 * q;
   u32x4 wf[TT][C];
 #pragma unroll
   for (int c = 0; c < C1; ++c)
@@ -177,45 +183,49 @@ void decode_gemm_kernel(DecodeGemmArgs a) {
       for (int sl = 0; sl < DG_WAVES; ++sl) s += red[((sl * TT + t) * 4 + i) * 64 + lane];
       v[t][i] = s;
     }
-  // lane holds columns col0 + 4 q .. +3 of token r
-  uint16_t *op = a.out + (int64_t)r * a.out_stride + col0 + 4 * q;
-  float o[4];
-  if constexpr (EPI == 1) {
-    const u32x2 old = *reinterpret_cast<const u32x2 *>(op);
-    o[0] = F16T::lo(old[0]) + v[0][0];
-    o[1] = F16T::hi(old[0]) + v[0][1];
-    o[2] = F16T::lo(old[1]) + v[0][2];
-    o[3] = F16T::hi(old[1]) + v[0][3];
-  } else if constexpr (EPI == 2) {
+  // lane holds rows 4 q .. +3 of each tile for token r: output columns
+  // col0 (+ t R) + 4 q .. +3, written as column pairs (rows < R only)
+  if (4 * q >= R) return;
+  constexpr int NOUT = EPI == 2 ? 1 : TT;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = silu_mul(v[0][i], v[TT - 1][i]);
-  } else {
+  for (int t = 0; t < NOUT; ++t) {
+    uint32_t *op = reinterpret_cast<uint32_t *>(a.out + (int64_t)r * a.out_stride + col0 + t * R +
+                                                4 * q);
+    float o[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = v[0][i];
+    for (int i = 0; i < 4; ++i) o[i] = EPI == 2 ? silu_mul(v[0][i], v[TT - 1][i]) : v[t][i];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      if (4 * q + 2 * h >= R) break;
+      float lo = o[2 * h], hi = o[2 * h + 1];
+      if constexpr (EPI == 1) {
+        const uint32_t old = op[h];
+        lo += F16T::lo(old);
+        hi += F16T::hi(old);
+      }
+      op[h] = pack2<F16T>(lo, hi);
+    }
   }
-  u32x2 pr;
-  pr[0] = pack2<F16T>(o[0], o[1]);
-  pr[1] = pack2<F16T>(o[2], o[3]);
-  *reinterpret_cast<u32x2 *>(op) = pr;
 }
 
-template <int EPI, int TT, int MP, bool NORM, int C>
+template <int EPI, int TT, int MP, bool NORM, int C, int R>
 void launch_dg(const DecodeGemmArgs &a, hipStream_t st) {
   // registers of the W fragments decide how many waves fit per SIMD; every
   // workgroup of a launch should be resident at once
   constexpr int WPE = TT * C <= 24 && MP == 8 ? 4 : 2;
-  decode_gemm_kernel<EPI, TT, MP, NORM, C, WPE><<<a.N / 16, DG_WAVES * 64, 0, st>>>(a);
+  const int grid = a.N / (EPI == 2 ? R : R * TT);
+  decode_gemm_kernel<EPI, TT, MP, NORM, C, WPE, R><<<grid, DG_WAVES * 64, 0, st>>>(a);
 }
 
-template <int EPI, int TT, int MP, bool NORM>
+template <int EPI, int TT, int MP, bool NORM, int R>
 int dispatch_k(const DecodeGemmArgs &a, int k, hipStream_t st) {
   switch (k) {
-    case 2048: launch_dg<EPI, TT, MP, NORM, 8>(a, st); return MCE_OK;
-    case 3072: launch_dg<EPI, TT, MP, NORM, 12>(a, st); return MCE_OK;
-    case 4096: launch_dg<EPI, TT, MP, NORM, 16>(a, st); return MCE_OK;
+    case 2048: launch_dg<EPI, TT, MP, NORM, 8, R>(a, st); return MCE_OK;
+    case 3072: launch_dg<EPI, TT, MP, NORM, 12, R>(a, st); return MCE_OK;
+    case 4096: launch_dg<EPI, TT, MP, NORM, 16, R>(a, st); return MCE_OK;
     case 8192:
       if constexpr (TT == 1 && !NORM && MP == 8) {  // 128 KB of staged x
-        launch_dg<EPI, TT, MP, NORM, 32>(a, st);
+        launch_dg<EPI, TT, MP, NORM, 32, R>(a, st);
         return MCE_OK;
       }
       break;
@@ -223,14 +233,60 @@ int dispatch_k(const DecodeGemmArgs &a, int k, hipStream_t st) {
   return MCE_ERR_UNSUPPORTED;
 }
 
+// Output columns per workgroup: R columns per tile times TT tiles (SwiGLU: R
+// gate / up column pairs).  The widest tile is kept unless a narrower one
+// cuts the columns of the busiest CU (whole rounds of workgroups over the
+// CUs times the columns per workgroup) by more than 10%: 3072 columns run as
+// 256 workgroups of 12, 5120 as 256 of 2 x 10, instead of 192 / 320 of 16.
+struct DgTile {
+  int r, tt;
+};
+
+DgTile pick_tile(int n, bool swiglu, int k) {
+  static const DgTile plain[] = {{16, 1}, {12, 1}, {10, 2}, {8, 1}};
+  static const DgTile glu[] = {{16, 2}, {8, 2}};
+  const int64_t cus = cu_count();
+  DgTile best = swiglu ? glu[0] : plain[0];
+  int64_t best_cost = -1;
+  const DgTile *cand = swiglu ? glu : plain;
+  const int n_cand = swiglu ? 2 : 4;
+  for (int i = 0; i < n_cand; ++i) {
+    const DgTile &t = cand[i];
+    if (t.tt == 2 && !swiglu && k == 8192) continue;  // one tile only at k = 8192
+    const int cols = swiglu ? t.r : t.r * t.tt;
+    if (n % cols != 0) continue;
+    const int64_t cost = ((n / cols) + cus - 1) / cus * cols;
+    if (best_cost < 0 || 10 * cost < 9 * best_cost) {
+      best = t;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
+template <int EPI, int MP, bool NORM>
+int dispatch_tile(const DecodeGemmArgs &a, int k, const DgTile &t, hipStream_t st) {
+  if constexpr (EPI == 2) {
+    return t.r == 8 ? dispatch_k<EPI, 2, MP, NORM, 8>(a, k, st) : dispatch_k<EPI, 2, MP, NORM, 16>(a, k, st);
+  } else {
+    switch (t.r) {
+      case 12: return dispatch_k<EPI, 1, MP, NORM, 12>(a, k, st);
+      case 10: return dispatch_k<EPI, 2, MP, NORM, 10>(a, k, st);
+      case 8: return dispatch_k<EPI, 1, MP, NORM, 8>(a, k, st);
+      default: return dispatch_k<EPI, 1, MP, NORM, 16>(a, k, st);
+    }
+  }
+}
+
 template <bool NORM>
 int dispatch(const DecodeGemmArgs &a, int k, int epilogue, hipStream_t st) {
   const bool small = a.M <= 8;
+  const DgTile t = pick_tile(a.N, epilogue == MCE_EPI_SWIGLU, k);
   if (epilogue == MCE_EPI_STORE)
-    return small ? dispatch_k<0, 1, 8, NORM>(a, k, st) : dispatch_k<0, 1, 16, NORM>(a, k, st);
+    return small ? dispatch_tile<0, 8, NORM>(a, k, t, st) : dispatch_tile<0, 16, NORM>(a, k, t, st);
   if (epilogue == MCE_EPI_ADD)
-    return small ? dispatch_k<1, 1, 8, NORM>(a, k, st) : dispatch_k<1, 1, 16, NORM>(a, k, st);
-  return small ? dispatch_k<2, 2, 8, NORM>(a, k, st) : dispatch_k<2, 2, 16, NORM>(a, k, st);
+    return small ? dispatch_tile<1, 8, NORM>(a, k, t, st) : dispatch_tile<1, 16, NORM>(a, k, t, st);
+  return small ? dispatch_tile<2, 8, NORM>(a, k, t, st) : dispatch_tile<2, 16, NORM>(a, k, t, st);
 }
 
 int decode_gemm_impl(const char *name, int dtype, const void *x, const void *norm_w, float eps,
