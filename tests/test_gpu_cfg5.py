@@ -150,3 +150,27 @@ def test_lm_head_rmsnorm_decode_gemm_at_vocab_128256(dev):
     out = rmsnorm_decode_gemm(x.to(dev), nw.to(dev), eps, w.to(dev)).float().cpu()
     err = (out - ref).abs()
     assert (err <= 2e-3 + 4e-3 * ref.abs()).all(), err.max().item()
+
+
+@pytest.mark.parametrize("m,k,norm", [(12, 3072, True), (5, 2048, False), (8, 4096, True),
+                                      (16, 2048, False)])
+def test_many_round_decode_gemm_matches_fp32(dev, m, k, norm):
+    """Launches of many rounds of workgroups (N = 65536: 4096 workgroups of 16
+    columns) take the 128-byte-row W loads with the fragments rebuilt through
+    LDS; every token-slot count, K and the fused / plain RMSNorm against fp32
+    torch (|err| <= 2e-3 + 4e-3 |ref|)."""
+    from mycustomcudaengine_amd.ops import decode_gemm, rmsnorm_decode_gemm
+    g = torch.Generator().manual_seed(51 + m + k)
+    n, eps = 65536, 1e-5
+    x = (torch.randn(m, k, generator=g) * 2).half()
+    nw = (1 + 0.1 * torch.randn(k, generator=g)).half()
+    w = (torch.randn(n, k, generator=g) * 0.02).half()
+    xf = x.float()
+    if norm:
+        xf = xf / torch.sqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * nw.float()
+        out = rmsnorm_decode_gemm(x.to(dev), nw.to(dev), eps, w.to(dev))
+    else:
+        out = decode_gemm(x.to(dev), w.to(dev))
+    ref = xf @ w.float().T
+    err = (out.float().cpu() - ref).abs()
+    assert (err <= 2e-3 + 4e-3 * ref.abs()).all(), err.max().item()
