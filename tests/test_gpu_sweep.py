@@ -10,6 +10,7 @@ with prefixes up to 2500 tokens, pages of 16-64 tokens, with and without the
 key split.
 """
 import math
+import os
 import random
 
 import pytest
@@ -21,7 +22,25 @@ from oracle.inputs import make_decode_case, make_prefill_case
 from oracle.ops_ref import decode_attention_ref, prefill_attention_ref, prefill_paged_ref
 
 TOL = 1e-2
+# MCE_SWEEP_CASES raises the number of seeds per family (defaults: 16 decode, 8 prefill)
+_N = os.environ.get("MCE_SWEEP_CASES")
+N_DECODE = int(_N) if _N else 16
+N_PREFILL = int(_N) if _N else 8
 pytestmark = pytest.mark.gpu
+
+
+def check_bar(out, ref, dtype, desc):
+    """fp16: max |err| <= 1e-2 of fp32 (the bar for this path).  bf16: the
+    reference test's allclose class, |err| <= 1e-2 + 1e-2 |ref|
+    (tests/test_paged_attention.py:86): rounding an exact result to bf16 alone
+    errs by up to 0.0078 in [2, 4) and 0.0156 in [4, 8), and the P weights
+    enter P.V in bf16, so a flat 1e-2 is not a bf16 bar."""
+    assert not torch.isnan(out).any(), desc
+    d = (out.float() - ref).abs()
+    if dtype == torch.bfloat16:
+        assert bool((d <= TOL + TOL * ref.abs()).all()), (desc, d.max().item())
+    else:
+        assert d.max().item() <= TOL, (desc, d.max().item())
 
 
 def _decode_config(i):
@@ -38,7 +57,7 @@ def _decode_config(i):
     return b, hkv, g, bs, dtype, ctx, extra
 
 
-@pytest.mark.parametrize("i", range(16))
+@pytest.mark.parametrize("i", range(N_DECODE))
 def test_decode_sweep(dev, i):
     b, hkv, g, bs, dtype, ctx, extra = _decode_config(i)
     need = max(1, max((c + bs - 1) // bs for c in ctx))
@@ -52,12 +71,10 @@ def test_decode_sweep(dev, i):
         case.block_size, case.scale).cpu()
     ref = decode_attention_ref(case.query, case.key_cache, case.value_cache,
                                case.block_tables, case.context_lens, case.scale)
-    assert not torch.isnan(out).any(), desc
-    err = (out.float() - ref).abs().max().item()
-    assert err <= TOL, (desc, err)
+    check_bar(out, ref, dtype, desc)
 
 
-@pytest.mark.parametrize("i", range(8))
+@pytest.mark.parametrize("i", range(N_PREFILL))
 def test_prefill_sweep(dev, i):
     r = random.Random(3000 + i)
     b, s = r.randint(1, 3), r.choice([1, r.randint(2, 64), r.randint(65, 900)])
@@ -69,9 +86,7 @@ def test_prefill_sweep(dev, i):
     out = ops.prefill_attention(case.query.to(dev), case.key.to(dev), case.value.to(dev),
                                 case.scale).cpu()
     ref = prefill_attention_ref(case.query, case.key, case.value, case.scale)
-    assert not torch.isnan(out).any(), desc
-    err = (out.float() - ref).abs().max().item()
-    assert err <= TOL, (desc, err)
+    check_bar(out, ref, dtype, desc)
 
 
 def _pool_case(r, prefixes, s, hq, hkv, bs, dtype):
@@ -96,7 +111,7 @@ def _pool_case(r, prefixes, s, hq, hkv, bs, dtype):
     return q, kc, vc, table, torch.tensor(ctx, dtype=torch.int32)
 
 
-@pytest.mark.parametrize("i", range(8))
+@pytest.mark.parametrize("i", range(N_PREFILL))
 def test_prefill_paged_sweep(dev, i):
     r = random.Random(5000 + i)
     b = r.randint(1, 3)
@@ -114,7 +129,5 @@ def test_prefill_paged_sweep(dev, i):
     args = (q.to(dev), kc.to(dev), vc.to(dev), table.to(dev), ctx.to(dev), scale)
     for split in (True, False):
         out = prefill_attention_paged(*args, split_keys=split).cpu()
-        assert not torch.isnan(out).any(), (desc, split)
         for j, ref in enumerate(refs):
-            err = (out[j].float() - ref).abs().max().item()
-            assert err <= TOL, (desc, split, j, err)
+            check_bar(out[j], ref, dtype, (desc, split, j))
