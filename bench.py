@@ -12,7 +12,9 @@ Extra fields on the same JSON line:
   prefill   cfg3 causal prefill (S=2048, 24/8 heads): algorithmic TFLOP/s
             (2 * D * Hq * S * (S+1)) and fraction of dense fp16 MFMA peak;
             the cfg3 pipeline's other legs beside it: RoPE in place of q and
-            k, the paged KV store of the 2048 tokens, and the two fused.
+            k, the paged KV store of the 2048 tokens, and the two fused; and
+            the reference's prefill benchmark (benchmark_prefill_attn.py: B=1,
+            S = 128 .. 2048) timed beside torch SDPA (causal, fused backends).
   splitk    cfg4 long-context decode (B=8, ctx 32768): GB/s.
   ref_harness  the reference's own decode harness shape (B=16, 32/32 heads,
             ctx 2048, ascending tables; tests/test_paged_attention.py:12-125)
@@ -257,6 +259,44 @@ def bench_harness(dev, steps: int, warmup: int) -> dict:
     log(f"reference harness: {out['us']} us ({out['gbs']} GB/s); SDPA {out.get('sdpa_us')} us")
     del mgr, k, v
     return out
+
+
+def bench_prefill_vs_sdpa(dev, steps: int) -> list:
+    """The reference's prefill benchmark (benchmarks/benchmark_prefill_attn.py:6-67): B=1,
+    24 / 8 heads, D=128, fp16 ~ N(0, 1), S = 128 .. 2048; prefill_attention timed beside
+    torch.nn.functional.scaled_dot_product_attention(is_causal=True) on the K/V
+    repeat-interleaved to 24 heads (its comparison), both with HIP events over back-to-back
+    calls after MFMA_WARMUP_CALLS warm-up calls; TFLOP/s over the causal pairs."""
+    import my_cuda_engine_cpp as ops
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    rows = []
+    g = torch.Generator(device=dev).manual_seed(44)
+    for s in (128, 256, 512, 1024, 2048):
+        q = torch.randn(1, s, 24, 128, generator=g, device=dev).half()
+        k = torch.randn(1, s, 8, 128, generator=g, device=dev).half()
+        v = torch.randn(1, s, 8, 128, generator=g, device=dev).half()
+        scale = 128 ** -0.5
+        flops = 2 * 128 * 24 * s * (s + 1)
+        ms = time_gpu(lambda: ops.prefill_attention(q, k, v, scale), steps, MFMA_WARMUP_CALLS,
+                      rounds=3)
+        row = {"seq_len": s, "us": round(ms * 1e3, 2),
+               "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+        qh = q.transpose(1, 2).contiguous()
+        kh = k.transpose(1, 2).repeat_interleave(3, dim=1).contiguous()
+        vh = v.transpose(1, 2).repeat_interleave(3, dim=1).contiguous()
+        try:
+            # fused backends only (no math fallback through batched GEMMs)
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                sms = time_gpu(lambda: torch.nn.functional.scaled_dot_product_attention(
+                    qh, kh, vh, is_causal=True, scale=scale), steps, MFMA_WARMUP_CALLS, rounds=3)
+            row["sdpa_us"] = round(sms * 1e3, 2)
+            row["speedup_vs_sdpa"] = round(sms / ms, 2)
+        except RuntimeError as e:  # no fused SDPA backend on this build
+            row["sdpa_us"] = None
+            row["sdpa_error"] = str(e)[:200]
+        rows.append(row)
+        log(f"prefill S={s}: {row['us']} us ({row['tflops']} TFLOP/s); SDPA {row.get('sdpa_us')} us")
+    return rows
 
 
 def bench_chunked(dev, steps: int, warmup: int) -> dict:
@@ -585,6 +625,7 @@ def main() -> None:
                                       "warm-up calls, HIP events",
                             "graph_us_per_call": round(pgms * 1e3, 2)}
         extra["prefill"]["legs"] = bench_prefill_legs(case3, dev, max(20, args.steps // 4), 5)
+        extra["prefill"]["vs_sdpa"] = bench_prefill_vs_sdpa(dev, max(20, args.steps // 4))
         torch.cuda.empty_cache()
         if not args.no_cpu:
             extra["prefill"]["cpu_baseline"] = cpu_baseline_prefill(case3)
