@@ -240,10 +240,10 @@ MCE_API int mce_rope_kv_store(int dtype, void *query, void *query_out, void *key
  *   MCE_EPI_SWIGLU w is [2n, k] (gate rows, then up rows);
  *                  out[:, j] = silu(x w_gate_j) * (x w_up_j)
  * x rows x_stride elements apart, out rows out_stride apart (out must not
- * overlap x).  Needs
+ * overlap x).  Needs dtype MCE_F16 (the engine's weights are fp16),
  * n % 16 == 0 and k in {2048, 3072, 4096}, or k == 8192 for m <= 8 without
- * SwiGLU; other shapes return MCE_ERR_UNSUPPORTED (callers then use a library
- * GEMM).
+ * SwiGLU; other dtypes and shapes return MCE_ERR_UNSUPPORTED (callers then
+ * use a library GEMM).
  * No single counterpart in the reference: its decode step runs these
  * projections through torch.matmul, then a separate SwiGLU kernel and
  * residual adds (engine/models/llama.py:94-110,143-165,174).

@@ -409,9 +409,9 @@ def decode_gemm(x: torch.Tensor, weight: torch.Tensor, out: torch.Tensor = None,
     [N, K] ([2N, K] gate rows then up rows for "swiglu").  epilogue "store"
     writes a new (or the given) [M, N] tensor; "add" accumulates into `out`
     in place (residual stream); "swiglu" returns silu(x W_gate^T) * x W_up^T.
-    Raises MCEError with code MCE_ERR_UNSUPPORTED for shapes the kernel does
-    not take (M > 16, N % 16, K outside {2048, 3072, 4096}, K = 8192 needs
-    M <= 8 and no SwiGLU); the engine then uses torch.matmul.  Engine-side op:
+    Raises MCEError with code MCE_ERR_UNSUPPORTED for inputs the kernel does
+    not take (other than fp16, M > 16, N % 16, K outside {2048, 3072, 4096},
+    K = 8192 needs M <= 8 and no SwiGLU); the engine then uses torch.matmul.  Engine-side op:
     the reference runs these projections through torch.matmul
     (engine/models/llama.py:94-174).
     """
