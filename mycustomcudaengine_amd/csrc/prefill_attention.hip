@@ -98,12 +98,6 @@ __device__ __forceinline__ float xor32_add(float x) {
   return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
 }
 
-#ifndef PF_SCHEDULE
-#define PF_SCHEDULE()
-#endif
-#ifndef PF_WAVES_PER_EU
-#define PF_WAVES_PER_EU 2
-#endif
 
 struct PrefillArgs {
   const uint16_t *q, *k, *v;
@@ -167,7 +161,9 @@ __device__ inline int prefill_parts(const PrefillArgs &a, int key_S, int item, i
 // item's key tiles and writes that part's partial softmax state instead of
 // the output; prefill_merge_kernel combines the parts.
 template <class T, int NRB, int KSPLIT, bool PAGED, bool SPLITK>
-__global__ __launch_bounds__(NRB * KSPLIT * 64) __attribute__((amdgpu_waves_per_eu(PF_WAVES_PER_EU, PF_WAVES_PER_EU)))
+// Two waves per SIMD (at most 256 registers each): one 8-wave workgroup per
+// CU, or two 4-wave workgroups.
+__global__ __launch_bounds__(NRB * KSPLIT * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_causal_kernel(PrefillArgs a) {
   static_assert(!SPLITK || (PAGED && KSPLIT == 2), "key parts: paged mode, two key streams");
   constexpr int BM = 32 * NRB;
@@ -546,7 +542,6 @@ void prefill_causal_kernel(PrefillArgs a) {
     const float mx = rowmax(s_nxt);
     load_k(kreg[set], u + 4);
     load_v(vreg[set], u + 3);
-    PF_SCHEDULE();
     if (__builtin_expect(__ballot(mx > thr) != 0, 0)) rescale(mx, s_nxt);
   };
   auto stage_only = [&](const int u, const int set) {
