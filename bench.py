@@ -21,6 +21,8 @@ Extra fields on the same JSON line:
             timed beside torch SDPA (fp16, contiguous K/V) on the same GPU.
   model     cfg5 Llama-3.2-3B random-init, B=8, prefill 512 then 128 greedy
             decode steps replayed via hipGraph: tok/s, ms/step, TTFT.
+  model_b1  the same at B=1, the shape the reference's engine benchmark
+            prints TTFT, inter-token latency and tok/s for.
   cpu_baseline  the CPU oracle on the same cfg2 inputs, on this host's cores
             (prefill, splitk and model carry their own: cfg3, cfg4, and a
             bounded cfg5 sample -- B=8 prefill of 32 tokens then 4 greedy
@@ -658,6 +660,15 @@ def main() -> None:
             log(f"cfg5 CPU baseline: {extra['model']['cpu_baseline']['value']} tok/s")
         log(f"cfg5 model: {extra['model']['tok_s']} tok/s, {extra['model']['ms_per_step']} ms/step "
             f"(host-prepared steps: {extra['model']['tok_s_host_prepared']} tok/s)")
+        torch.cuda.empty_cache()
+        # the reference's own engine benchmark shape: one sequence
+        # (benchmarks/benchmark_engine.py:198-271: TTFT, inter-token latency, tok/s)
+        m1 = bench_model(dev, batch=1, cpu=False)
+        m1["workload"] = ("reference engine benchmark shape: Llama-3.2-3B random-init fp16, B=1, "
+                          "prefill 512, 128 greedy decode steps replayed via hipGraph")
+        extra["model_b1"] = m1
+        log(f"B=1 model: TTFT {m1['ttft_ms']} ms, ITL {m1['itl_ms_synced']} ms, {m1['tok_s']} tok/s "
+            f"(host-prepared steps: {m1['tok_s_host_prepared']} tok/s)")
         torch.cuda.empty_cache()
 
     if args.only == "chunked":
