@@ -195,6 +195,24 @@ def test_rejects_bad_inputs(dev):
                                    case.scale)
 
 
+@pytest.mark.parametrize("b,hi,mb", [(2048, 64, 72), (700, 300, 72), (700, 400, 25)])
+def test_large_batches(dev, b, hi, mb):
+    """Batches past one pass of the split partition's context-length prefix
+    sum (512 sequences per pass, up to the 2048 sequences a call takes), with
+    empty rows mixed in: the split mode (table capacity 1152 tokens) and the
+    per-sequence mode (400), on a NaN-filled pool."""
+    g = torch.Generator().manual_seed(700 + b + hi)
+    ctxs = torch.randint(0, hi + 1, (b,), generator=g).tolist()
+    check(make_decode_case(71 + b, b, ctxs, max_blocks=mb), dev)
+
+
+def test_rejects_batch_over_limit(dev):
+    """2049 sequences exceed what one call takes: an error before any launch."""
+    case = make_decode_case(72, 2049, [1] * 2049)
+    with pytest.raises(RuntimeError, match="batch 2049"):
+        run_gpu(case, dev)
+
+
 @pytest.mark.parametrize("ctxs,mb", [([512], None), ([3000, 129, 2048, 4096], None),
                                      ([600] * 8, 48), ([9000, 700], 1024), ([0, 33, 1], 4)])
 def test_bf16(dev, ctxs, mb):
