@@ -235,11 +235,13 @@ def test_prefill_bf16_matches_oracle(dev, b, s, hq, hkv):
     assert err <= TOL, err
 
 
-@pytest.mark.parametrize("b,s", [(8, 512), (6, 700)])
+@pytest.mark.parametrize("b,s", [(8, 512), (6, 700), (64, 16), (128, 5), (48, 43)])
 def test_prefill_large_grid_matches_oracle(dev, b, s):
     """Grids of at least two workgroups per CU take the kernel without the
-    in-workgroup key split (the small cases above take the split one)."""
-    case = make_prefill_case(60 + s, b, s)
+    in-workgroup key split (the small cases above take the split one),
+    including many short prompts in one call (items of one sequence's
+    few rows, partial last items)."""
+    case = make_prefill_case(60 + s + b, b, s)
     out = ops.prefill_attention(case.query.to(dev), case.key.to(dev), case.value.to(dev),
                                 case.scale).cpu()
     ref = prefill_attention_ref(case.query, case.key, case.value, case.scale)
