@@ -69,6 +69,51 @@ def test_prefill_then_eager_decode_match_oracle(dev, projections, monkeypatch):
         tok = want.argmax(-1, keepdim=True).to(dev)  # follow the oracle's greedy path
 
 
+def test_one_token_prompt_and_reused_pages(dev):
+    """A one-token prompt (prefill of S = 1) then decode steps match the
+    oracle; then a finished sequence is freed and a new one is allocated on
+    exactly its pages, which still hold the old sequence's K/V, and its
+    prefill and decode steps match the oracle too: only the new sequence's own
+    positions are ever read."""
+    gen, v = 3, CFG["vocab_size"]
+    w_cpu = random_llama_weights(CFG, seed=8, norm_std=0.1)
+    weights = {k: t.to(dev) for k, t in w_cpu.items()}
+    per_seq = (40 + gen + 15) // 16
+    cache = KVCacheManager(num_blocks=2 * per_seq, block_size=16,
+                           num_layers=CFG["num_hidden_layers"], num_heads=8, head_dim=128,
+                           device=dev)
+    model = Llama3BEngineModel(Llama3BConfig(CFG), weights, cache)
+    ref = LlamaRef(CFG, w_cpu)
+    g = torch.Generator().manual_seed(9)
+
+    def run(seq, prompt_len):
+        ids = torch.randint(0, v, (1, prompt_len), generator=g)
+        logits = prefill_step(model, ids.to(dev), [seq])
+        close(logits, ref.prefill(ids, [seq]))
+        tok = logits.argmax(-1, keepdim=True)
+        for i in range(gen):
+            pos = prompt_len + i
+            slots = torch.from_numpy(cache.slot_mapping([seq], [pos + 1])).to(dev)
+            mb = len(cache.block_tables[seq])
+            out = model.decode_step(tok, torch.full((1, 1), pos, dtype=torch.int32, device=dev),
+                                    torch.full((1,), pos + 1, dtype=torch.int32, device=dev),
+                                    slots, cache.get_block_table_tensor([seq], mb), mb)
+            want = ref.decode(tok.cpu(), [pos], [seq])
+            close(out, want)
+            tok = want.argmax(-1, keepdim=True).to(dev)
+
+    cache.allocate_sequence(0, 40 + gen)
+    cache.allocate_sequence(1, 40 + gen)
+    assert not cache.free_blocks  # the pool is exactly the two sequences
+    run(0, 40)   # fills its pages with K/V
+    run(1, 1)    # one-token prompt
+    old = list(cache.block_tables[0])
+    cache.free_sequence(0)
+    cache.allocate_sequence(5, 20 + gen)
+    assert cache.block_tables[5] == old[:len(cache.block_tables[5])]
+    run(5, 20)   # on the freed pages
+
+
 def test_graph_replay_matches_eager(dev):
     b, s, steps = 3, 20, 6
     model, cache, _ = build(dev, b, s, steps + 1, seed=6)
