@@ -41,7 +41,9 @@
 //
 // Per wave and 32-token tile, with the next tile's K/V loads in flight while
 // the current tile is computed:
-//   * the segment's physical block ids are staged in LDS;
+//   * the segment's physical block ids are staged in LDS; each wave's first
+//     tile reads its ids straight from the table row, so its K/V loads
+//     leave before the staging's LDS writes and barrier;
 //   * lane group lg (16 lanes) owns tokens 8 lg .. 8 lg + 7 of the tile and
 //     lane lr owns dims 8 lr .. 8 lr + 7: every K and V load instruction reads
 //     four whole 256-byte token rows (the pattern that streams fastest on
@@ -107,16 +109,19 @@ struct DecodeArgs {
 __device__ inline int clamp_ctx(int c, int cap) { return c < 0 ? 0 : (c > cap ? cap : c); }
 
 // Exclusive prefix sum of per-sequence split weights (tiles + SEG_TILES for a
-// non-empty sequence) into pre[0..B]; returns NT.  Sequence b's real tiles
+// non-empty sequence) into pre[0..B], and the clamped context lengths into
+// ctx_out[0..B) (so the segments do not load them again); returns NT.  Sequence b's real tiles
 // are [pre[b] + SEG_TILES, pre[b+1]).
 template <int NW>
-__device__ int build_tile_prefix(const DecodeArgs &a, int *pre, int *wave_tot) {
+__device__ int build_tile_prefix(const DecodeArgs &a, int *pre, int *wave_tot, int *ctx_out) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int cap = a.maxb << a.bs_log2;
   int carry = 0;
   for (int base = 0; base < a.B; base += NW * 64) {
     const int b = base + tid;
-    int v = b < a.B ? (clamp_ctx(a.ctx_lens[b], cap) + TILE - 1) / TILE : 0;
+    const int cb = b < a.B ? clamp_ctx(a.ctx_lens[b], cap) : 0;
+    if (b < a.B) ctx_out[b] = cb;
+    int v = (cb + TILE - 1) / TILE;
     if (v > 0) v += SEG_TILES;
     int incl = v;
 #pragma unroll
@@ -226,6 +231,7 @@ void paged_decode_kernel(DecodeArgs a) {
   __shared__ int pre[MAX_BATCH + 1];
   __shared__ int wave_tot[NW];
   __shared__ int blk_lds[MAX_IDS];
+  __shared__ int ctx_lds[MAX_BATCH];
   const int nb_hi = (int)(a.num_blocks - 1 < 0x7fffffff ? a.num_blocks - 1 : 0x7fffffff);
   __shared__ float red_acc[NW][G][HD];
   __shared__ float red_m[NW][G], red_l[NW][G];
@@ -294,7 +300,7 @@ void paged_decode_kernel(DecodeArgs a) {
     }
   } else {
     seg0 = SEG_TILES;
-    NT = build_tile_prefix<NW>(a, pre, wave_tot);
+    NT = build_tile_prefix<NW>(a, pre, wave_tot, ctx_lds);
     je = partition_count(NT, a.J);
   }
   if (!a.per_seq && j == 0) {
@@ -339,7 +345,7 @@ void paged_decode_kernel(DecodeArgs a) {
   for (; b < a.B && pre[b] < t_hi; ++b) {
     const int r0 = pre[b] + seg0;  // first real tile of b in the split space
     if (pre[b + 1] == pre[b] || max(t_lo, r0) >= min(t_hi, pre[b + 1])) continue;
-    const int ctx = a.per_seq ? ctx_j : clamp_ctx(a.ctx_lens[b], cap);
+    const int ctx = a.per_seq ? ctx_j : ctx_lds[b];
     const int seg_lo = max(t_lo, r0) - r0;             // tile index in b
     const int seg_hi = min(t_hi, pre[b + 1]) - r0;
     const int tok_lo = seg_lo * TILE;
@@ -379,30 +385,46 @@ void paged_decode_kernel(DecodeArgs a) {
       // ids[blk - first_blk]: physical block of logical block blk of b (the
       // per-sequence mode staged the whole row at the start)
       const int first_blk = a.per_seq ? 0 : s_lo >> bs_log2;
-      if (!a.per_seq) {
-        const int nblk = ((t_end - 1) >> bs_log2) - first_blk + 1;
-        lds_barrier();  // previous users of blk_lds are done
-        for (int i = tid; i < nblk; i += NTH) {
-          const int v = bt[first_blk + i];
-          blk_lds[i] = v < 0 ? 0 : (v > nb_hi ? nb_hi : v);
-        }
-        lds_barrier();
-      }
-      if (!active) continue;
+      const int ntile = (t_end - s_lo + TILE - 1) / TILE;
 
       // ---- loads of one tile: lane group lg owns tokens t0 + 8 lg .. +7 (one
       // block, since bs >= 8); each K and V row is one 256-byte run read by
       // 16 lanes x 16 bytes ----
-      auto load_tile = [&](int t0, u32x4 (&kk)[8], u32x4 (&vv)[8]) {
-        int tv = t0 + 8 * lg;
-        tv = tv < t_end ? tv : t0;
-        const int64_t phys = blk_lds[(tv >> bs_log2) - first_blk];
+      auto load_rows = [&](int64_t phys, int tv, u32x4 (&kk)[8], u32x4 (&vv)[8]) {
         const int64_t off = ((phys << bs_log2) + (tv & (bs - 1))) * slot_stride + lr * 8;
 #pragma unroll
         for (int s8 = 0; s8 < 8; ++s8) kk[s8] = ld_nt(kbase + off + s8 * slot_stride);
 #pragma unroll
         for (int s8 = 0; s8 < 8; ++s8) vv[s8] = ld_nt(vbase + off + s8 * slot_stride);
       };
+      auto load_tile = [&](int t0, u32x4 (&kk)[8], u32x4 (&vv)[8]) {
+        int tv = t0 + 8 * lg;
+        tv = tv < t_end ? tv : t0;
+        load_rows(blk_lds[(tv >> bs_log2) - first_blk], tv, kk, vv);
+      };
+      u32x4 kA[8], kB[8], vA[8], vB[8];
+      int k = rlane;
+      if (!a.per_seq) {
+        const int nblk = ((t_end - 1) >> bs_log2) - first_blk + 1;
+        lds_barrier();  // previous users of blk_lds are done
+        // The wave's first tile does not wait for the staging: each lane
+        // group reads its block id straight from the table row, issued before
+        // the segment's ids (loads return in order), and its K / V loads leave
+        // before the staging's LDS writes and barrier.
+        const int t0f = k < ntile ? s_lo + TILE * k : s_lo;
+        int tv0 = t0f + 8 * lg;
+        tv0 = tv0 < t_end ? tv0 : t0f;
+        const int id0 = bt[tv0 >> bs_log2];
+        const int st0 = bt[first_blk + (tid < nblk ? tid : nblk - 1)];
+        if (active && k < ntile) load_rows(id0 < 0 ? 0 : (id0 > nb_hi ? nb_hi : id0), tv0, kA, vA);
+        if (tid < nblk) blk_lds[tid] = st0 < 0 ? 0 : (st0 > nb_hi ? nb_hi : st0);
+        for (int i = tid + NTH; i < nblk; i += NTH) {
+          const int v = bt[first_blk + i];
+          blk_lds[i] = v < 0 ? 0 : (v > nb_hi ? nb_hi : v);
+        }
+        lds_barrier();
+      }
+      if (!active) continue;
       // ---- compute of one tile ----
       auto tile_body = [&](int t0, u32x4 (&kk)[8], u32x4 (&vv)[8]) {
         const int tv = t0 + 8 * lg;
@@ -510,10 +532,7 @@ void paged_decode_kernel(DecodeArgs a) {
       };
 
       // ---- software-pipelined tile loop: next tile's loads before compute ----
-      const int ntile = (t_end - s_lo + TILE - 1) / TILE;
-      u32x4 kA[8], kB[8], vA[8], vB[8];
-      int k = rlane;
-      if (k < ntile) load_tile(s_lo + TILE * k, kA, vA);
+      if (a.per_seq && k < ntile) load_tile(s_lo + TILE * k, kA, vA);
       if constexpr (FUSED) {
         // (per-sequence mode: every wave of the workgroup is active and
         // reaches this barrier)  RoPE of the query rows and, by wave 0, of the
