@@ -245,6 +245,7 @@ void paged_decode_kernel(DecodeArgs a) {
   RopeCS cs_new{};
   u32x4 kx_new{}, vx_new{}, q_pre[G];
   __shared__ u32x4 knv_lds[32];  // rotated k (lanes 0-15) and v (16-31) of the new token
+  u32x4 kA[8], vA[8];  // the wave's first tile (fused mode: fetched in the prologue)
   if (a.per_seq) {
     seg0 = 0;
     // one workgroup per (head group, sequence j): a one-sequence tile space
@@ -254,6 +255,16 @@ void paged_decode_kernel(DecodeArgs a) {
     // together with its context length.
     // (maxb <= PER_SEQ_MAX_TOKENS / MIN_BS <= NTH: one block id per thread)
     const int32_t *btj = a.btab + (int64_t)j * a.maxb;
+    // Fused mode: the wave's first tile (tile rlane) does not wait for the
+    // staging.  Each lane group reads its block id straight from the table
+    // row (the first load issued), and the tile's K/V loads leave once the
+    // prologue's other loads are issued (position first, so the cos / sin
+    // fetch goes out before the K/V).  Tokens past the context are masked by
+    // the tile computation; the row index stays in the table.  (The plain
+    // kernel measured no faster this way: it stages first.)
+    const int tvf = TILE * rlane + 8 * lg;
+    const int idf = FUSED ? btj[min(tvf >> bs_log2, a.maxb - 1)] : 0;
+    if constexpr (FUSED) pos_j = a.positions[j];
     const int bt_v = tid < a.maxb ? btj[tid] : 0;
     ctx_j = clamp_ctx(a.ctx_lens[j], cap);
     if constexpr (FUSED) {
@@ -264,7 +275,6 @@ void paged_decode_kernel(DecodeArgs a) {
       // tile's loads are issued (tile loop below).  The stores are not waited
       // for: every K / V row the workgroup loads from the new slot is taken
       // from the LDS copy, which is what reading after the store returns.
-      pos_j = a.positions[j];
       const int64_t sl = a.slots[j];
       slot_j = sl >= 0 && sl < a.num_slots ? sl : -1;
       rope_ok = pos_j >= 0 && pos_j < a.table_rows;
@@ -276,6 +286,15 @@ void paged_decode_kernel(DecodeArgs a) {
         q_pre[h] = *reinterpret_cast<const u32x4 *>(a.query + (int64_t)j * a.q_stride_b +
                                                     (int64_t)(head0 + h) * HD + lr * 8);
       if (rope_ok) cs_new = rope_fetch(a, pos_j, lr);
+    }
+    if constexpr (FUSED) {
+      const int64_t phys = idf < 0 ? 0 : (idf > nb_hi ? nb_hi : idf);
+      const int64_t ss = (int64_t)a.Hkv * HD;
+      const int64_t off = ((phys << bs_log2) + (tvf & (bs - 1))) * ss + (int64_t)g * HD + lr * 8;
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) kA[s8] = ld_nt(a.kcache + off + s8 * ss);
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) vA[s8] = ld_nt(a.vcache + off + s8 * ss);
     }
     if (tid < a.maxb) blk_lds[tid] = bt_v < 0 ? 0 : (bt_v > nb_hi ? nb_hi : bt_v);
     if (tid == 0) {
@@ -402,7 +421,7 @@ void paged_decode_kernel(DecodeArgs a) {
         tv = tv < t_end ? tv : t0;
         load_rows(blk_lds[(tv >> bs_log2) - first_blk], tv, kk, vv);
       };
-      u32x4 kA[8], kB[8], vA[8], vB[8];
+      u32x4 kB[8], vB[8];
       int k = rlane;
       if (!a.per_seq) {
         const int nblk = ((t_end - 1) >> bs_log2) - first_blk + 1;
@@ -532,7 +551,7 @@ void paged_decode_kernel(DecodeArgs a) {
       };
 
       // ---- software-pipelined tile loop: next tile's loads before compute ----
-      if (a.per_seq && k < ntile) load_tile(s_lo + TILE * k, kA, vA);
+      if (!FUSED && a.per_seq && k < ntile) load_tile(s_lo + TILE * k, kA, vA);
       if constexpr (FUSED) {
         // (per-sequence mode: every wave of the workgroup is active and
         // reaches this barrier)  RoPE of the query rows and, by wave 0, of the
