@@ -323,3 +323,63 @@ def test_cfg2_repeat_calls_identical(dev):
     first = run_gpu(case, dev)
     for _ in range(3):
         assert torch.equal(run_gpu(case, dev), first)
+
+
+@pytest.mark.parametrize("pad", ["minus_one", "past_pool", "nan_block"])
+@pytest.mark.parametrize("mb", [40, 80])
+def test_padded_tables_short_contexts(dev, pad, mb):
+    """Table entries past a sequence's blocks are never used: padding of -1,
+    ids past the pool, or ids of NaN-filled pool blocks leave the result
+    unchanged.  The fused per-sequence kernel reads each wave's first tile's
+    block id straight from the table row, also for tiles past a short context
+    (waves 1-7 of a 1-token sequence); the split mode (capacity 1280 tokens,
+    mb = 80) reads ids inside the context only.  Plain decode against the
+    oracle (mb = 40: per-sequence mode, 80: split), fused decode against the
+    separate ops bit for bit and against the oracle on the updated cache."""
+    d, bs, b, rows = 128, 16, 8, 1400
+    ctx = [1, 5, 16, 17, 33, 100, 255, 257]
+    case = make_decode_case(140 + mb, b, ctx, max_blocks=mb)
+    pool = case.key_cache.shape[0]
+    bt = case.block_tables.clone()
+    used = {int(v) for i, c in enumerate(ctx) for v in bt[i, :(c + bs - 1) // bs]}
+    nan_ids = [i for i in range(pool) if i not in used]
+    assert nan_ids and torch.isnan(case.key_cache[nan_ids[0]]).all()
+    fill = {"minus_one": -1, "past_pool": pool + 12345, "nan_block": nan_ids[0]}[pad]
+    for i, c in enumerate(ctx):
+        bt[i, (c + bs - 1) // bs:] = fill
+    padded = type(case)(case.query, case.key_cache, case.value_cache, bt, case.context_lens,
+                        case.block_size, case.scale)
+    check(padded, dev)
+    if mb * bs > 1024:
+        return  # the fused kernel takes tables of at most 1024 tokens
+    gen = torch.Generator().manual_seed(141)
+    pos = torch.tensor([c - 1 for c in ctx], dtype=torch.int32)
+    slots = torch.tensor([int(bt[i, (c - 1) // bs]) * bs + (c - 1) % bs for i, c in enumerate(ctx)],
+                         dtype=torch.int32)
+    inv = 1.0 / (500000.0 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    ang = torch.outer(torch.arange(rows, dtype=torch.float32), inv)
+    cos, sin = ang.cos().contiguous(), ang.sin().contiguous()
+    hq, hkv = 24, 8
+    qkv = torch.randn(b, (hq + 2 * hkv) * d, generator=gen).half()
+    to = lambda t: t.to(dev)
+    cos_d, sin_d, pos_d, slots_d, bt_d, cl_d = map(to, (cos, sin, pos, slots, bt, case.context_lens))
+
+    def views(buf):
+        return (buf[:, :hq * d].view(b, hq, d), buf[:, hq * d:(hq + hkv) * d].view(b, hkv, d),
+                buf[:, (hq + hkv) * d:].view(b, hkv, d))
+
+    qkv1, kc1, vc1 = to(qkv.clone()), to(case.key_cache.clone()), to(case.value_cache.clone())
+    out1 = decode_rope_attention(*views(qkv1), kc1, vc1, cos_d, sin_d, pos_d, slots_d, bt_d, cl_d,
+                                 mb, case.scale)
+    qkv2, kc2, vc2 = to(qkv.clone()), to(case.key_cache.clone()), to(case.value_cache.clone())
+    q_rot = torch.empty(b, hq, d, dtype=torch.float16, device=dev)
+    rope_kv_store(*views(qkv2), kc2, vc2, cos_d, sin_d, pos_d, slots_d, query_out=q_rot)
+    out2 = ops.paged_attention_decode(q_rot, kc2, vc2, bt_d, cl_d, mb, bs, case.scale)
+    torch.cuda.synchronize()
+    bits = lambda t: t.view(torch.int16)
+    assert torch.equal(bits(out1), bits(out2))
+    assert torch.equal(bits(kc1), bits(kc2)) and torch.equal(bits(vc1), bits(vc2))
+    ref = decode_attention_ref(q_rot.cpu(), kc1.cpu(), vc1.cpu(), bt, case.context_lens, case.scale)
+    out = out1.cpu()
+    assert not torch.isnan(out).any()
+    assert (out.float() - ref).abs().max().item() <= TOL
