@@ -39,8 +39,10 @@
 //   fences, which on gfx950 write back the L2 per workgroup; the kernel
 //   boundary gives the same visibility for free.)
 //
-// Per wave and 32-token tile, with the next tile's K/V loads in flight while
-// the current tile is computed:
+// Per wave and 32-token tile; a wave fetches its next tile once the current
+// one is computed (one tile in flight per wave: with a workgroup of 8 waves
+// on every CU that is ~32 MB in flight across the chip, and a second tile in
+// flight per wave measured slower):
 //   * the segment's physical block ids are staged in LDS; each wave's first
 //     tile reads its ids straight from the table row, so its K/V loads
 //     leave before the staging's LDS writes and barrier;
@@ -421,7 +423,6 @@ void paged_decode_kernel(DecodeArgs a) {
         tv = tv < t_end ? tv : t0;
         load_rows(blk_lds[(tv >> bs_log2) - first_blk], tv, kk, vv);
       };
-      u32x4 kB[8], vB[8];
       int k = rlane;
       if (!a.per_seq) {
         const int nblk = ((t_end - 1) >> bs_log2) - first_blk + 1;
@@ -550,7 +551,7 @@ void paged_decode_kernel(DecodeArgs a) {
         tile_body(t0, kk, vv);
       };
 
-      // ---- software-pipelined tile loop: next tile's loads before compute ----
+      // ---- tile loop: compute the tile in registers, then fetch the wave's next ----
       if (!FUSED && a.per_seq && k < ntile) load_tile(s_lo + TILE * k, kA, vA);
       if constexpr (FUSED) {
         // (per-sequence mode: every wave of the workgroup is active and
@@ -576,15 +577,9 @@ void paged_decode_kernel(DecodeArgs a) {
         lds_barrier();
       }
       while (k < ntile) {
-        int kn = k + wph;
-        if (kn < ntile) load_tile(s_lo + TILE * kn, kB, vB);
         compute_tile(s_lo + TILE * k, kA, vA);
-        k = kn;
-        if (k >= ntile) break;
-        kn = k + wph;
-        if (kn < ntile) load_tile(s_lo + TILE * kn, kA, vA);
-        compute_tile(s_lo + TILE * k, kB, vB);
-        k = kn;
+        k += wph;
+        if (k < ntile) load_tile(s_lo + TILE * k, kA, vA);
       }
     }
 
