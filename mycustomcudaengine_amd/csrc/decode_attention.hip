@@ -2,7 +2,7 @@
 // csrc/kernels/flash_attn_paged.cu:25-142, host wrapper :144-168).
 //
 // Work decomposition: balanced split-K (flash-decoding) over the whole batch.
-//   Every sequence's context is cut into 32-token tiles and the tiles of all
+//   Every sequence's context is cut into 16-token tiles and the tiles of all
 //   sequences are laid end to end (sequence b owns tiles [pre[b], pre[b+1]),
 //   the first SEG_TILES of them virtual: they weight the cost of a segment).
 //   The grid has J workgroups per group of kv heads (about one workgroup per
@@ -39,16 +39,17 @@
 //   fences, which on gfx950 write back the L2 per workgroup; the kernel
 //   boundary gives the same visibility for free.)
 //
-// Per wave and 32-token tile; a wave fetches its next tile once the current
-// one is computed (one tile in flight per wave: with a workgroup of 8 waves
-// on every CU that is ~32 MB in flight across the chip, and a second tile in
-// flight per wave measured slower):
+// Per wave and 16-token tile; a wave fetches its next tile once the current
+// one is computed.  One 8 KB tile in flight per wave (with a workgroup of 8
+// waves on every CU, ~16 MB across the chip) covers the memory latency and
+// streams faster than more: 32-token tiles, or a second tile in flight per
+// wave, measured slower, and 8-token tiles slower again:
 //   * the segment's physical block ids are staged in LDS; each wave's first
 //     tile reads its ids straight from the table row, so its K/V loads
 //     leave before the staging's LDS writes and barrier;
-//   * lane group lg (16 lanes) owns tokens 8 lg .. 8 lg + 7 of the tile and
-//     lane lr owns dims 8 lr .. 8 lr + 7: every K and V load instruction reads
-//     four whole 256-byte token rows (the pattern that streams fastest on
+//   * lane group lg (16 lanes) owns tokens TPG lg .. TPG lg + TPG - 1 of the
+//     tile and lane lr owns dims 8 lr .. 8 lr + 7: every K and V load
+//     instruction reads four whole 256-byte token rows (the pattern that streams fastest on
 //     MI355X; loading K in an MFMA-operand layout, 64-byte pieces of 16 rows
 //     per instruction, measured ~6% slower);
 //   * scores: v_dot2_f32_f16 (v_dot2_f32_bf16 for bf16) over the lane's dims
@@ -64,19 +65,20 @@
 namespace mce {
 
 constexpr int HD = 128;           // head_dim
-constexpr int TILE = 32;          // tokens per wave iteration
+constexpr int TILE = 16;          // tokens per wave iteration
+constexpr int TPG = TILE / 4;     // tokens per 16-lane group
 constexpr int DEC_NW = 8;         // waves per workgroup
 constexpr int NT_THREADS = DEC_NW * 64;
 constexpr int MIN_BS = 8;
 constexpr int MAX_IDS = 2048;     // block ids staged in LDS at a time
 constexpr int MAX_BATCH = 2048;   // sequences per call (LDS prefix array)
-constexpr int MIN_TILES_PER_WG = 2;
+constexpr int MIN_TILES_PER_WG = 4;
 // Split weight of a sequence start, in tiles: starting a segment (query and
-// block-id loads, pipeline refill, one more partial) costs one to two tiles of
+// block-id loads, pipeline refill, one more partial) costs two to four tiles of
 // streaming, so every non-empty sequence is preceded by SEG_TILES virtual
 // tiles in the split space and a workgroup that takes a boundary gets that
 // many fewer real tiles.
-constexpr int SEG_TILES = 1;
+constexpr int SEG_TILES = 2;
 // Context capacities up to this many tokens take the per-sequence mode.
 constexpr int PER_SEQ_MAX_TOKENS = 1024;
 
@@ -247,7 +249,7 @@ void paged_decode_kernel(DecodeArgs a) {
   RopeCS cs_new{};
   u32x4 kx_new{}, vx_new{}, q_pre[G];
   __shared__ u32x4 knv_lds[32];  // rotated k (lanes 0-15) and v (16-31) of the new token
-  u32x4 kA[8], vA[8];  // the wave's first tile (fused mode: fetched in the prologue)
+  u32x4 kA[TPG], vA[TPG];  // the wave's first tile (fused mode: fetched in the prologue)
   if (a.per_seq) {
     seg0 = 0;
     // one workgroup per (head group, sequence j): a one-sequence tile space
@@ -264,7 +266,7 @@ void paged_decode_kernel(DecodeArgs a) {
     // fetch goes out before the K/V).  Tokens past the context are masked by
     // the tile computation; the row index stays in the table.  (The plain
     // kernel measured no faster this way: it stages first.)
-    const int tvf = TILE * rlane + 8 * lg;
+    const int tvf = TILE * rlane + TPG * lg;
     const int idf = FUSED ? btj[min(tvf >> bs_log2, a.maxb - 1)] : 0;
     if constexpr (FUSED) pos_j = a.positions[j];
     const int bt_v = tid < a.maxb ? btj[tid] : 0;
@@ -294,9 +296,9 @@ void paged_decode_kernel(DecodeArgs a) {
       const int64_t ss = (int64_t)a.Hkv * HD;
       const int64_t off = ((phys << bs_log2) + (tvf & (bs - 1))) * ss + (int64_t)g * HD + lr * 8;
 #pragma unroll
-      for (int s8 = 0; s8 < 8; ++s8) kA[s8] = ld_nt(a.kcache + off + s8 * ss);
+      for (int s8 = 0; s8 < TPG; ++s8) kA[s8] = ld_nt(a.kcache + off + s8 * ss);
 #pragma unroll
-      for (int s8 = 0; s8 < 8; ++s8) vA[s8] = ld_nt(a.vcache + off + s8 * ss);
+      for (int s8 = 0; s8 < TPG; ++s8) vA[s8] = ld_nt(a.vcache + off + s8 * ss);
     }
     if (tid < a.maxb) blk_lds[tid] = bt_v < 0 ? 0 : (bt_v > nb_hi ? nb_hi : bt_v);
     if (tid == 0) {
@@ -408,18 +410,18 @@ void paged_decode_kernel(DecodeArgs a) {
       const int first_blk = a.per_seq ? 0 : s_lo >> bs_log2;
       const int ntile = (t_end - s_lo + TILE - 1) / TILE;
 
-      // ---- loads of one tile: lane group lg owns tokens t0 + 8 lg .. +7 (one
-      // block, since bs >= 8); each K and V row is one 256-byte run read by
+      // ---- loads of one tile: lane group lg owns tokens t0 + TPG lg .. + TPG - 1
+      // (one block, since bs >= 8); each K and V row is one 256-byte run read by
       // 16 lanes x 16 bytes ----
-      auto load_rows = [&](int64_t phys, int tv, u32x4 (&kk)[8], u32x4 (&vv)[8]) {
+      auto load_rows = [&](int64_t phys, int tv, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG]) {
         const int64_t off = ((phys << bs_log2) + (tv & (bs - 1))) * slot_stride + lr * 8;
 #pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8) kk[s8] = ld_nt(kbase + off + s8 * slot_stride);
+        for (int s8 = 0; s8 < TPG; ++s8) kk[s8] = ld_nt(kbase + off + s8 * slot_stride);
 #pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8) vv[s8] = ld_nt(vbase + off + s8 * slot_stride);
+        for (int s8 = 0; s8 < TPG; ++s8) vv[s8] = ld_nt(vbase + off + s8 * slot_stride);
       };
-      auto load_tile = [&](int t0, u32x4 (&kk)[8], u32x4 (&vv)[8]) {
-        int tv = t0 + 8 * lg;
+      auto load_tile = [&](int t0, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG]) {
+        int tv = t0 + TPG * lg;
         tv = tv < t_end ? tv : t0;
         load_rows(blk_lds[(tv >> bs_log2) - first_blk], tv, kk, vv);
       };
@@ -432,7 +434,7 @@ void paged_decode_kernel(DecodeArgs a) {
         // the segment's ids (loads return in order), and its K / V loads leave
         // before the staging's LDS writes and barrier.
         const int t0f = k < ntile ? s_lo + TILE * k : s_lo;
-        int tv0 = t0f + 8 * lg;
+        int tv0 = t0f + TPG * lg;
         tv0 = tv0 < t_end ? tv0 : t0f;
         const int id0 = bt[tv0 >> bs_log2];
         const int st0 = bt[first_blk + (tid < nblk ? tid : nblk - 1)];
@@ -446,13 +448,13 @@ void paged_decode_kernel(DecodeArgs a) {
       }
       if (!active) continue;
       // ---- compute of one tile ----
-      auto tile_body = [&](int t0, u32x4 (&kk)[8], u32x4 (&vv)[8]) {
-        const int tv = t0 + 8 * lg;
+      auto tile_body = [&](int t0, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG]) {
+        const int tv = t0 + TPG * lg;
         // scores: 4 v_dot2 over the lane's 8 dims, then a 16-lane DPP sum;
         // every lane of a group ends with the scores of the group's 8 tokens
-        float sc[8][G];
+        float sc[TPG][G];
 #pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8)
+        for (int s8 = 0; s8 < TPG; ++s8)
 #pragma unroll
           for (int h = 0; h < G; ++h) {
             float d = 0.f;
@@ -469,8 +471,9 @@ void paged_decode_kernel(DecodeArgs a) {
         bool rescale = false;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-          float mx = fmaxf(fmaxf(fmaxf(sc[0][h], sc[1][h]), fmaxf(sc[2][h], sc[3][h])),
-                           fmaxf(fmaxf(sc[4][h], sc[5][h]), fmaxf(sc[6][h], sc[7][h])));
+          float mx = sc[0][h];
+#pragma unroll
+          for (int s8 = 1; s8 < TPG; ++s8) mx = fmaxf(mx, sc[s8][h]);
           mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
           mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
           mx = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, mx)));
@@ -479,14 +482,14 @@ void paged_decode_kernel(DecodeArgs a) {
           rescale |= mn != m_run[h];
           m_run[h] = mn;
         }
-        float p[8][G];
+        float p[TPG][G];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
           // (s - m) c rather than one FMA: exactly 0 at the max, so a single
           // token gets p = 1 and the output is v itself
           float ps = 0.f;
 #pragma unroll
-          for (int s8 = 0; s8 < 8; ++s8) {
+          for (int s8 = 0; s8 < TPG; ++s8) {
             p[s8][h] = fast_exp2((sc[s8][h] - m_run[h]) * c);
             ps += p[s8][h];
           }
@@ -500,11 +503,11 @@ void paged_decode_kernel(DecodeArgs a) {
         }
         // tokens past the end: zero their V rows (p is 0, V may be NaN garbage)
 #pragma unroll
-        for (int s8 = 0; s8 < 8; ++s8)
+        for (int s8 = 0; s8 < TPG; ++s8)
           if (tv + s8 >= t_end) vv[s8] = u32x4{0, 0, 0, 0};
         // acc += P V over token pairs with v_dot2 (p packed in the element type)
 #pragma unroll
-        for (int sp = 0; sp < 4; ++sp) {
+        for (int sp = 0; sp < TPG / 2; ++sp) {
           uint32_t pp[G];
 #pragma unroll
           for (int h = 0; h < G; ++h) pp[h] = T::pack_p(p[2 * sp][h], p[2 * sp + 1][h]);
@@ -526,20 +529,20 @@ void paged_decode_kernel(DecodeArgs a) {
       // the slot is patched, in place, every row by a select (a conditional
       // write of one row would become an indexed register write, which puts
       // the tile in scratch memory).
-      auto compute_tile = [&](int t0, u32x4 (&kk)[8], u32x4 (&vv)[8]) {
+      auto compute_tile = [&](int t0, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG]) {
         int sub = -1;
         if (FUSED && slot_j >= 0) {
-          const int tv = t0 + 8 * lg;
+          const int tv = t0 + TPG * lg;
           const int tvc = tv < t_end ? tv : t0;
           const int64_t slot0 =
               ((int64_t)blk_lds[(tvc >> bs_log2) - first_blk] << bs_log2) + (tvc & (bs - 1));
           const int64_t dd = slot_j - slot0;
-          sub = dd >= 0 && dd < 8 ? (int)dd : -1;
+          sub = dd >= 0 && dd < TPG ? (int)dd : -1;
         }
         if (__builtin_expect(__ballot(sub >= 0) != 0, 0)) {
           const u32x4 kn = knv_lds[lr], vn = knv_lds[16 + lr];
 #pragma unroll
-          for (int s8 = 0; s8 < 8; ++s8) {
+          for (int s8 = 0; s8 < TPG; ++s8) {
             const bool hit = s8 == sub;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
