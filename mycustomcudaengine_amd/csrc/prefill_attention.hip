@@ -31,8 +31,7 @@
 // straight-line block as the softmax and P V of tile k, so the exp/convert
 // VALU work of one tile runs while the matrix cores work on the other.  K and
 // V^T are double-buffered in LDS (K one tile ahead of V) with one barrier per
-// tile; tiles are fetched into registers two tiles ahead of their staging
-// (one tile ahead in the paged mode).
+// tile; each tile is fetched into registers one step before it is staged.
 //
 // Softmax in the log2 domain: Q is pre-scaled by c = scale log2(e) when it is
 // loaded, and each score accumulator starts at -m (the row's running max, in
@@ -236,7 +235,7 @@ void prefill_causal_kernel(PrefillArgs a) {
   // piece pc -> key pc / 16, 16-byte column pc % 16 (16 lanes per key row),
   // the same for K and V.
   // Loads are unconditional buffer loads (straight-line code keeps the
-  // compiler's vmcnt accounting exact, so staging waits only for the set it
+  // compiler's vmcnt accounting exact, so staging waits only for the tile it
   // stores) with loop-invariant per-thread offsets; the hardware range check
   // of the buffer descriptor returns zeros for keys at or past the sequence
   // end (the descriptor spans this (batch, kv head)'s rows up to key S).
@@ -268,14 +267,13 @@ void prefill_causal_kernel(PrefillArgs a) {
   };
   using KRegs = u32x4[KP];
   using VRegs = u32x4[KP];
-  // Register sets of staged tiles in flight: two in the contiguous mode (a
-  // tile is fetched two steps before it is staged); one in the paged mode,
-  // whose page-offset arithmetic would otherwise spill (fetched one step
-  // ahead; measured 4-10% faster than two sets with spills).
-  constexpr int NSETS = PAGED ? 1 : 2;
-  constexpr int AHEAD = NSETS + 2;  // the K tile fetched at step u is u + AHEAD
-  KRegs kreg[NSETS];
-  VRegs vreg[NSETS];
+  // One register set of staged tiles in flight (each tile fetched one step
+  // before it is staged): a second set, fetching two steps ahead, measured
+  // 2-2.5% slower in the contiguous mode and 4-10% in the paged mode (whose
+  // page-offset arithmetic then spilled).
+  constexpr int AHEAD = 3;  // the K tile fetched at step u is u + AHEAD
+  KRegs kreg;
+  VRegs vreg;
   auto load_k = [&](KRegs &dst, int u) {
     if constexpr (PAGED) {
 #pragma unroll
@@ -455,19 +453,13 @@ void prefill_causal_kernel(PrefillArgs a) {
 
   // Prologue (per key stream): K_0 staged and scored (prepared in s_a); K_1
   // and V_0 staged into the second
-  // / first buffers; (K_2, V_1) fetched into register set 0, then (with two
-  // sets) (K_3, V_2) into set 1, so each staging step below waits only for
-  // the older set (indices are stream indices u).
+  // / first buffers; (K_2, V_1) fetched into the staging registers (indices
+  // are stream indices u).
   store_k(k0, ks_h);
   lds_barrier();
-  load_k(kreg[0], 2);
-  load_v(vreg[0], 1);
+  load_k(kreg, 2);
+  load_v(vreg, 1);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (NSETS == 2) {
-    load_k(kreg[NSETS - 1], 3);
-    load_v(vreg[NSETS - 1], 2);
-    __builtin_amdgcn_sched_barrier(0);
-  }
   {
     scores(ks_h, 0.f, s_a);
     prep(s_a, tb + kh);
@@ -481,20 +473,20 @@ void prefill_causal_kernel(PrefillArgs a) {
   //   A: scores of tile u + 1 (K in buffer (u+1)%2, accumulators starting at
   //      -m_run) on the matrix cores while the exp2 / convert / row-sum work
   //      of tile u runs on the VALU;
-  //   K_{u+2} / V_{u+1} are staged from register set u%NSETS into the
+  //   K_{u+2} / V_{u+1} are staged from the staging registers into the
   //      buffers that iteration u - 1 finished reading;
   //   B: P V of tile u (V^T in buffer u%2) while tile u + 1 is masked (DIAG)
-  //      and max-reduced; then K_{u+AHEAD} / V_{u+AHEAD-1} are fetched into
-  //      register set u%NSETS;
+  //      and max-reduced; then K_{u+3} / V_{u+2} are fetched into the
+  //      staging registers;
   // rows whose max grew are rescaled after the block.  The mask is applied
   // only by the DIAG form (tiles that reach the diagonal or the sequence end),
   // and waves past their last tile only stage (stage_only), so the three
   // loops below keep every step free of branches.  Barriers match by count:
   // every wave runs the same (even) number of iterations.  Staging is
-  // unconditional, so the loop carries the register sets without copies (a
+  // unconditional, so the loop carries the staging registers without copies (a
   // copy of a pending load would wait for every load in flight); tiles past
   // the end are zero-filled and written to buffers nobody reads again.
-  auto step = [&](const int u, const int set, floatx16 &s_cur, floatx16 &s_nxt, auto diag) {
+  auto step = [&](const int u, floatx16 &s_cur, floatx16 &s_nxt, auto diag) {
     constexpr bool DIAG = decltype(diag)::value;
     lds_barrier();
     const int kt = tb + KSPLIT * u + kh;  // key tile
@@ -531,8 +523,8 @@ void prefill_causal_kernel(PrefillArgs a) {
       l_i = T::dot2(pp, ones, l_i);
       pk[e2 >> 2][e2 & 3] = pp;
     }
-    store_k(kreg[set % NSETS], ks_h + (u & 1) * KS_SIZE);
-    store_v(vreg[set % NSETS], vs_h + ((u + 1) & 1) * VS_SIZE);
+    store_k(kreg, ks_h + (u & 1) * KS_SIZE);
+    store_v(vreg, vs_h + ((u + 1) & 1) * VS_SIZE);
     // ---- B
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
@@ -549,16 +541,16 @@ void prefill_causal_kernel(PrefillArgs a) {
         if (8 * (e >> 2) + (e & 3) > l2) s_nxt[e] = -INFINITY;
     }
     const float mx = rowmax(s_nxt);
-    load_k(kreg[set % NSETS], u + AHEAD);
-    load_v(vreg[set % NSETS], u + AHEAD - 1);
+    load_k(kreg, u + AHEAD);
+    load_v(vreg, u + AHEAD - 1);
     if (__builtin_expect(__ballot(mx > thr) != 0, 0)) rescale(mx, s_nxt);
   };
-  auto stage_only = [&](const int u, const int set) {
+  auto stage_only = [&](const int u) {
     lds_barrier();
-    store_k(kreg[set % NSETS], ks_h + (u & 1) * KS_SIZE);
-    store_v(vreg[set % NSETS], vs_h + ((u + 1) & 1) * VS_SIZE);
-    load_k(kreg[set % NSETS], u + AHEAD);
-    load_v(vreg[set % NSETS], u + AHEAD - 1);
+    store_k(kreg, ks_h + (u & 1) * KS_SIZE);
+    store_v(vreg, vs_h + ((u + 1) & 1) * VS_SIZE);
+    load_k(kreg, u + AHEAD);
+    load_v(vreg, u + AHEAD - 1);
   };
   // step u needs the mask from u_first on (its next tile KSPLIT (u+1) + kh
   // reaches n_full); tile KSPLIT u + kh is past this wave's rows from u_end on
@@ -571,16 +563,16 @@ void prefill_causal_kernel(PrefillArgs a) {
   const std::integral_constant<bool, true> diag;
   int u = 0;
   for (; u < u1; u += 2) {
-    step(u, 0, s_a, s_b, plain);
-    step(u + 1, 1, s_b, s_a, plain);
+    step(u, s_a, s_b, plain);
+    step(u + 1, s_b, s_a, plain);
   }
   for (; u < u2; u += 2) {
-    step(u, 0, s_a, s_b, diag);
-    step(u + 1, 1, s_b, s_a, diag);
+    step(u, s_a, s_b, diag);
+    step(u + 1, s_b, s_a, diag);
   }
   for (; u < n_iter; u += 2) {
-    stage_only(u, 0);
-    stage_only(u + 1, 1);
+    stage_only(u);
+    stage_only(u + 1);
   }
 
   // ---- epilogue: merge the key streams (KSPLIT = 2), normalise, store.
