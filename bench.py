@@ -153,7 +153,7 @@ def bench_decode(case, dev, steps, warmup, rounds=1):
     ms = time_gpu(fn, steps, warm, rounds)
     graph_ms = time_graph_batch(fn)
     nbytes = case.algorithmic_bytes()
-    return ms, nbytes, nbytes / (ms * 1e-3) / 1e9, graph_ms
+    return ms, nbytes, nbytes / (ms * 1e-3) / 1e9, graph_ms, warm
 
 
 # Warm-up calls before an MFMA-bound workload is timed: after memory-bound
@@ -620,10 +620,10 @@ def main() -> None:
     if args.only in (None, "decode"):
         log("generating cfg2 inputs")
         case2 = cfg2_decode()
-        ms, nbytes, gbs, graph_ms = bench_decode(case2, dev, args.steps, args.warmup)
+        ms, nbytes, gbs, graph_ms, warm2 = bench_decode(case2, dev, args.steps, args.warmup)
         log(f"cfg2 decode: {ms * 1e3:.1f} us/step ({gbs:.1f} GB/s); in a 20-call hipGraph "
             f"{graph_ms * 1e3:.1f} us/step")
-        result["decode"] = (ms, nbytes, gbs, graph_ms)
+        result["decode"] = (ms, nbytes, gbs, graph_ms, warm2)
 
     extra = {}
     if args.only in (None, "prefill"):
@@ -651,7 +651,7 @@ def main() -> None:
     if args.only in (None, "splitk"):
         log("generating cfg4 inputs")
         case4 = cfg4_decode()
-        kms, kbytes, kgbs, _ = bench_decode(case4, dev, max(20, args.steps // 4), 5, rounds=5)
+        kms, kbytes, kgbs, _, _ = bench_decode(case4, dev, max(20, args.steps // 4), 5, rounds=5)
         log(f"cfg4 split-K decode: {kms * 1e3:.1f} us, {kgbs:.1f} GB/s")
         extra["splitk"] = {"workload": "cfg4 paged decode B=8 ctx=32768 24/8 heads D=128",
                            "us": round(kms * 1e3, 2), "bytes": kbytes,
@@ -697,7 +697,7 @@ def main() -> None:
         cpu = cpu_baseline_decode(case2)
         log(f"CPU baseline: {cpu['value']} GB/s on {cpu['cores']} cores")
 
-    ms, nbytes, gbs, graph_ms = result["decode"]
+    ms, nbytes, gbs, graph_ms, warm2 = result["decode"]
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -720,7 +720,9 @@ def main() -> None:
                      "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "timing": {"method": "K back-to-back op calls from Python (decode kernel + LSE "
-                             "merge kernel each), HIP events on the launch stream",
+                             "merge kernel each), HIP events on the launch stream, after "
+                             f"{warm2} warm-up calls (W, and at least {DECODE_WARMUP_MS:.0f} ms "
+                             "of calls)",
                    "graph_us_per_step": round(graph_ms * 1e3, 2),
                    "graph": "20 op calls captured in one hipGraph, replayed; per call",
                    "algorithmic_bytes_per_step": nbytes},
