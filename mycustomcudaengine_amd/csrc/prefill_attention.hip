@@ -489,6 +489,10 @@ void prefill_causal_kernel(PrefillArgs a) {
   auto step = [&](const int u, floatx16 &s_cur, floatx16 &s_nxt, auto diag) {
     constexpr bool DIAG = decltype(diag)::value;
     lds_barrier();
+    // LLVM's built-in MFMA / LDS-read interleaving strategy for the step's
+    // block (same instructions, another order): 1-2% faster at every shape
+    // measured, with fewer registers.
+    __builtin_amdgcn_iglp_opt(0);
     const int kt = tb + KSPLIT * u + kh;  // key tile
     const uint16_t *kp = &ks_h[((u + 1) & 1) * KS_SIZE + r32 * KS_PITCH + 8 * hf];
     // V^T fragment (dt, kk): lane l = 16 q + s of group q takes dims 32 dt +
