@@ -6,8 +6,9 @@ GB/s: every K/V byte once, q and out once, the block-table entries used.
 One "step" = one paged_attention_decode call over the whole batch, inputs
 resident in HBM.  Timed with HIP events on the launch stream over K
 back-to-back calls, after W warm-up calls and at least DECODE_WARMUP_MS of
-them (the same op captured in a hipGraph and replayed is timed too and
-reported beside it).
+them; `value` is the median of 5 such windows, each started behind a few
+queued untimed calls (the same op captured in a hipGraph and replayed is
+timed too and reported beside it).
 
 Extra fields on the same JSON line:
   prefill   cfg3 causal prefill (S=2048, 24/8 heads): algorithmic TFLOP/s
@@ -20,21 +21,24 @@ Extra fields on the same JSON line:
   ref_harness  the reference's own decode harness shape (B=16, 32/32 heads,
             ctx 2048, ascending tables; tests/test_paged_attention.py:12-125)
             timed beside torch SDPA (fp16, contiguous K/V) on the same GPU.
+  norms     RMSNorm at the reference's harness shape (8 x 2048 x 4096,
+            tests/test_ops.py:17-61) and cfg5's 4096 x 3072, SwiGLU at
+            [4096, 16384]: us, GB/s, fraction of HBM peak, beside torch.
   model     cfg5 Llama-3.2-3B random-init, B=8, prefill 512 then 128 greedy
             decode steps replayed via hipGraph: tok/s, ms/step, TTFT.
   model_b1  the same at B=1, the shape the reference's engine benchmark
             prints TTFT, inter-token latency and tok/s for.
   cpu_baseline  the CPU oracle on the same cfg2 inputs, on this host's cores
             (prefill, splitk and model carry their own: cfg3, cfg4, and a
-            bounded cfg5 sample -- B=8 prefill of 32 tokens then 4 greedy
-            steps of the fp32 model oracle).
+            bounded cfg5 sample -- B=8 prefill of the 512-token prompts then 4
+            greedy steps at positions 512-515 of the fp32 model oracle).
 
   chunked   (--only chunked; not in the default run) chunked prefill from the
             page pool, B=1 chunk 512 behind 0-7680 cached tokens and B=4 chunk
             128 behind 2048, with and without the key split: us, TFLOP/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--only decode|prefill|splitk|harness|model|chunked]
+                       [--only decode|prefill|legs|splitk|harness|norms|model|chunked]
 (--only runs one workload; only the default run prints the full result line.)
 """
 from __future__ import annotations
@@ -61,12 +65,21 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_gpu(fn, steps: int, warmup: int, rounds: int = 1) -> float:
+# Untimed calls issued in front of every timing window: the start event is
+# recorded behind them, so it fires while the GPU is already busy and the host
+# is ahead of it; the window then holds the K calls' GPU time, not the host's
+# latency to its first launch (~15 us of Python per call, which 20 calls of a
+# 55 us kernel would otherwise average in).
+LEAD_CALLS = 5
+
+
+def time_gpu(fn, steps: int, warmup: int, rounds: int = 5) -> float:
     """Average ms per call of fn(), issued eagerly from Python, measured with
-    HIP events on the current stream over `steps` back-to-back calls (includes
-    host launch overhead when the GPU work is shorter than the Python call).
-    rounds > 1: the median of that many such windows (the first windows after
-    other work can run at lower clocks)."""
+    HIP events on the current stream over `steps` back-to-back calls after
+    LEAD_CALLS queued untimed ones (the host's per-call work still counts
+    whenever the GPU work is shorter than the Python call).  The median of
+    `rounds` such windows (the first windows after other work can run at lower
+    clocks)."""
     for _ in range(warmup):
         fn()
     stream = torch.cuda.current_stream()
@@ -75,6 +88,8 @@ def time_gpu(fn, steps: int, warmup: int, rounds: int = 1) -> float:
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         stop = torch.cuda.Event(enable_timing=True)
+        for _ in range(LEAD_CALLS):
+            fn()
         start.record(stream)
         for _ in range(steps):
             fn()
@@ -134,21 +149,22 @@ def cpu_info() -> dict:
 # Warm-up of a decode benchmark, in milliseconds of back-to-back calls: the
 # first milliseconds of load after the GPU idled (input generation on the host)
 # run at lower clocks (measured: cfg2 57.2-57.5 us per call after 100 warm-up
-# calls, 55.2-55.3 us after 2000, equal to the graph-replayed figure).
-DECODE_WARMUP_MS = 100.0
+# calls, 55.2-55.3 us after 2000 ~ 110 ms, equal to the graph-replayed figure).
+DECODE_WARMUP_MS = 250.0
 
 
-def bench_decode(case, dev, steps, warmup, rounds=1):
+def bench_decode(case, dev, steps, warmup, rounds=5):
     """Decode attention on `case`: back-to-back eager op calls (decode kernel +
     merge kernel) timed with HIP events after at least DECODE_WARMUP_MS of
-    warm-up calls, plus the same call captured 20 times in one hipGraph."""
+    warm-up calls (the median of `rounds` windows of `steps` calls), plus the
+    same call captured 20 times in one hipGraph."""
     import my_cuda_engine_cpp as ops
     q = case.query.to(dev)
     kc, vc = case.key_cache.to(dev), case.value_cache.to(dev)
     bt, cl = case.block_tables.to(dev), case.context_lens.to(dev)
     fn = lambda: ops.paged_attention_decode(q, kc, vc, bt, cl, case.max_blocks,
                                             case.block_size, case.scale)
-    probe = time_gpu(fn, 10, 2)  # ms per call, to size the warm-up
+    probe = time_gpu(fn, 10, 2, rounds=1)  # ms per call, to size the warm-up
     warm = max(warmup, int(DECODE_WARMUP_MS / max(probe, 1e-3)))
     ms = time_gpu(fn, steps, warm, rounds)
     graph_ms = time_graph_batch(fn)
@@ -224,6 +240,70 @@ def bench_prefill_legs(case, dev, steps, warmup) -> dict:
                      "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "eager_us": round(eager_ms * 1e3, 2)}
         log(f"cfg3 {name}: {out[name]['us']} us, {out[name]['gbs']} GB/s")
+    return out
+
+
+def bench_norms(dev, steps: int, warmup: int, compiled: bool = False) -> dict:
+    """RMSNorm and SwiGLU, the reference's only ops with published kernel figures
+    (rmsnorm_report.txt:2-12: 811.84 us, 88.67 % of DRAM for 8 x 2048 x 4096 fp16).
+    RMSNorm at the reference harness shape (tests/test_ops.py:17-61:
+    [8, 2048, 4096] fp16, eps 1e-5) and at cfg5's prefill rows (8 x 512 tokens x
+    3072); SwiGLU at cfg5's prefill gate_up [4096, 16384] -> [4096, 8192].  Each
+    timed with HIP events over back-to-back eager calls (median of 5 windows),
+    beside what the reference compares with on the same GPU: torch's fused
+    F.rms_norm (nn.RMSNorm) and the unfused eager formula, F.silu(g) * u for
+    SwiGLU, and with `compiled` torch.compile of the unfused RMSNorm (a Triton
+    kernel; --only norms).  Algorithmic bytes: the input read once, the output
+    written once, plus the weight row."""
+    import my_cuda_engine_cpp as ops
+    g = torch.Generator(device=dev).manual_seed(48)
+    out = {}
+
+    def rate(nbytes, ms):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+                "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+    for name, shape in (("rmsnorm_ref_harness", (8, 2048, 4096)), ("rmsnorm_cfg5_prefill",
+                                                                   (8, 512, 3072))):
+        h = shape[-1]
+        x = torch.randn(*shape, generator=g, device=dev).half()
+        w = (1.0 + 0.1 * torch.randn(h, generator=g, device=dev)).half()
+        nbytes = 2 * x.numel() * 2 + h * 2
+        ms = time_gpu(lambda: ops.rmsnorm(x, w, 1e-5), steps, warmup)
+        row = {"shape": list(shape), "bytes": nbytes, **rate(nbytes, ms)}
+        nms = time_gpu(lambda: torch.nn.functional.rms_norm(x, (h,), w, 1e-5), steps, warmup)
+        row["torch_rms_norm_us"] = round(nms * 1e3, 2)
+        row["speedup_vs_torch_rms_norm"] = round(nms / ms, 2)
+
+        def unfused(x_):
+            return x_ * torch.rsqrt(x_.pow(2).mean(-1, keepdim=True) + 1e-5) * w
+        ums = time_gpu(lambda: unfused(x), steps, warmup)
+        row["unfused_eager_us"] = round(ums * 1e3, 2)
+        if compiled:
+            try:
+                cfn = torch.compile(unfused)
+                cfn(x)
+                cms = time_gpu(lambda: cfn(x), steps, warmup)
+                row["torch_compile_us"] = round(cms * 1e3, 2)
+                row["speedup_vs_torch_compile"] = round(cms / ms, 2)
+            except Exception as e:  # no working compiler backend on this box
+                row["torch_compile_error"] = str(e)[:200]
+        out[name] = row
+        log(f"{name}: {row['us']} us ({row['gbs']} GB/s); torch rms_norm {row['torch_rms_norm_us']} us")
+        del x
+    t, inter = 4096, 8192
+    gu = torch.randn(t, 2 * inter, generator=g, device=dev).half()
+    nbytes = gu.numel() * 2 + t * inter * 2
+    ms = time_gpu(lambda: ops.swiglu(gu), steps, warmup)
+    row = {"shape": [t, 2 * inter], "bytes": nbytes, **rate(nbytes, ms)}
+    gate, up = gu[:, :inter], gu[:, inter:]
+    tms = time_gpu(lambda: torch.nn.functional.silu(gate) * up, steps, warmup)
+    row["torch_silu_mul_us"] = round(tms * 1e3, 2)
+    row["speedup_vs_torch"] = round(tms / ms, 2)
+    out["swiglu_cfg5_prefill"] = row
+    log(f"swiglu: {row['us']} us ({row['gbs']} GB/s); torch silu*up {row['torch_silu_mul_us']} us")
+    del gu
     return out
 
 
@@ -453,13 +533,16 @@ def bench_model(dev, steps: int = 128, batch: int = 8, prompt: int = 512, seed: 
             "cpu_baseline": cpu_base}
 
 
-def cpu_baseline_model(cfg, weights: dict, ids: torch.Tensor, prompt: int = 32,
+def cpu_baseline_model(cfg, weights: dict, ids: torch.Tensor, prompt: int = 512,
                        steps: int = 4) -> dict:
-    """A bounded cfg5 sample on the CPU: the fp32 model oracle (oracle/model_ref.py)
-    with the benchmark's own weights (copied to the host as fp32) prefills the
-    first `prompt` tokens of the benchmark's 8 prompts, then takes `steps`
-    greedy decode steps.  value = decode tokens/s (8 sequences x steps over the
-    decode wall time); the prefill time is reported beside it."""
+    """A bounded cfg5 sample on the CPU, on the planned workload
+    (benchmarks/benchmark_engine.py:226-268): the fp32 model oracle
+    (oracle/model_ref.py) with the benchmark's own weights (copied to the host
+    as fp32) prefills the benchmark's 8 prompts of `prompt` tokens, then takes
+    `steps` greedy decode steps at positions prompt .. prompt + steps - 1, so
+    each step pays attention over cfg5's context as the GPU steps do.  value =
+    decode tokens/s (8 sequences x steps over the decode wall time); the
+    prefill time is reported beside it."""
     from oracle.model_ref import LlamaRef
     n = len(os.sched_getaffinity(0))
     torch.set_num_threads(n)
@@ -483,11 +566,12 @@ def cpu_baseline_model(cfg, weights: dict, ids: torch.Tensor, prompt: int = 32,
     decode_s = time.perf_counter() - t0
     info = cpu_info()
     return {"value": round(b * steps / decode_s, 3), "unit": "tok/s", "cores": n, "kind": "port",
+            "prompt": prompt, "decode_steps": steps,
             "prefill_ms": round(prefill_s * 1e3, 1),
             "ms_per_step": round(decode_s / steps * 1e3, 1),
             "sample": f"cfg5 geometry with the benchmark's weights, fp32 torch model oracle: "
-                      f"B={b} prefill of {prompt} tokens ({prefill_s * 1e3:.0f} ms), then "
-                      f"{steps} greedy decode steps ({decode_s / steps * 1e3:.0f} ms/step, "
+                      f"B={b} prefill of prompt {prompt} ({prefill_s * 1e3:.0f} ms), then "
+                      f"k={steps} greedy decode steps ({decode_s / steps * 1e3:.0f} ms/step, "
                       f"positions {prompt}-{prompt + steps - 1}); {info['cpu_model']}; "
                       f"torch {info['torch']}"}
 
@@ -587,8 +671,8 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "prefill", "legs", "splitk", "harness", "model",
-                                       "chunked"],
+    ap.add_argument("--only", choices=["decode", "prefill", "legs", "splitk", "harness", "norms",
+                                       "model", "chunked"],
                     default=None)
     ap.add_argument("--calibration-copy", action="store_true",
                     help="first copy 256 MiB device-to-device (a kernel of known traffic, "
@@ -666,6 +750,11 @@ def main() -> None:
         extra["ref_harness"] = bench_harness(dev, max(20, args.steps // 4), 5)
         torch.cuda.empty_cache()
 
+    if args.only in (None, "norms"):
+        extra["norms"] = bench_norms(dev, max(20, args.steps // 4), 20,
+                                     compiled=args.only == "norms")
+        torch.cuda.empty_cache()
+
     if args.only in (None, "model"):
         log("cfg5 Llama-3.2-3B decode")
         extra["model"] = bench_model(dev, cpu=not args.no_cpu)
@@ -722,7 +811,9 @@ def main() -> None:
         "timing": {"method": "K back-to-back op calls from Python (decode kernel + LSE "
                              "merge kernel each), HIP events on the launch stream, after "
                              f"{warm2} warm-up calls (W, and at least {DECODE_WARMUP_MS:.0f} ms "
-                             "of calls)",
+                             f"of calls); the median of 5 windows of K calls, each behind "
+                             f"{LEAD_CALLS} queued untimed calls",
+                   "warmup_calls": warm2, "windows": 5, "lead_calls": LEAD_CALLS,
                    "graph_us_per_step": round(graph_ms * 1e3, 2),
                    "graph": "20 op calls captured in one hipGraph, replayed; per call",
                    "algorithmic_bytes_per_step": nbytes},

@@ -50,7 +50,12 @@ enum { MCE_EPI_STORE = 0, MCE_EPI_ADD = 1, MCE_EPI_SWIGLU = 2 };
 /* Message of the last failed call on this host thread ("" if none). */
 MCE_API const char *mce_last_error(void);
 
-/* ABI version (major * 100 + minor). */
+/*
+ * ABI version (major * 100 + minor) of the library; callers built against
+ * this header should check mce_abi_version() == MCE_ABI_VERSION.
+ * 101: mce_argmax_rows takes (workspace, workspace_bytes) before the stream.
+ */
+#define MCE_ABI_VERSION 101
 MCE_API int mce_abi_version(void);
 
 /*

@@ -28,6 +28,9 @@ MCE_ERR_WORKSPACE = 4
 MCE_F16 = 0
 MCE_BF16 = 1
 MCE_DECODE_NOALLOC_SCRATCH_BYTES = 16 << 20
+# MCE_ABI_VERSION of include/mce_abi.h: the argument lists in SIGNATURES
+# below are those of this version, so load() refuses a library of another.
+MCE_ABI_VERSION = 101
 
 _c_int, _c_i64, _c_f, _c_sz, _vp = (
     ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p)
@@ -120,6 +123,11 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
+        version = lib.mce_abi_version()
+        if version != MCE_ABI_VERSION:
+            raise ImportError(
+                f"{LIB_PATH} has ABI version {version}, this binding expects "
+                f"{MCE_ABI_VERSION}; rebuild with `python -m mycustomcudaengine_amd.build`")
         runtimes = _hip_runtimes_mapped()
         if len(runtimes) > 1:
             raise ImportError(

@@ -482,16 +482,21 @@ void paged_decode_kernel(DecodeArgs a) {
           rescale |= mn != m_run[h];
           m_run[h] = mn;
         }
-        float p[TPG][G];
+        // p packed in the element type for P V (v_dot2 over token pairs); the
+        // row sum is taken from the same packed values (v_dot2 against 1.0),
+        // so numerator and denominator use the one rounded p
+        const uint32_t ones = T::pack_p(1.0f, 1.0f);
+        uint32_t pp[TPG / 2][G];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
           // (s - m) c rather than one FMA: exactly 0 at the max, so a single
           // token gets p = 1 and the output is v itself
           float ps = 0.f;
 #pragma unroll
-          for (int s8 = 0; s8 < TPG; ++s8) {
-            p[s8][h] = fast_exp2((sc[s8][h] - m_run[h]) * c);
-            ps += p[s8][h];
+          for (int sp = 0; sp < TPG / 2; ++sp) {
+            pp[sp][h] = T::pack_p(fast_exp2((sc[2 * sp][h] - m_run[h]) * c),
+                                  fast_exp2((sc[2 * sp + 1][h] - m_run[h]) * c));
+            ps = T::dot2(pp[sp][h], ones, ps);
           }
           l_grp[h] = l_grp[h] * alpha[h] + ps;
         }
@@ -505,20 +510,17 @@ void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int s8 = 0; s8 < TPG; ++s8)
           if (tv + s8 >= t_end) vv[s8] = u32x4{0, 0, 0, 0};
-        // acc += P V over token pairs with v_dot2 (p packed in the element type)
+        // acc += P V over token pairs with v_dot2
 #pragma unroll
         for (int sp = 0; sp < TPG / 2; ++sp) {
-          uint32_t pp[G];
-#pragma unroll
-          for (int h = 0; h < G; ++h) pp[h] = T::pack_p(p[2 * sp][h], p[2 * sp + 1][h]);
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
             const uint32_t lo = __builtin_amdgcn_perm(vv[2 * sp + 1][k], vv[2 * sp][k], 0x05040100u);
             const uint32_t hi = __builtin_amdgcn_perm(vv[2 * sp + 1][k], vv[2 * sp][k], 0x07060302u);
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-              acc[h][2 * k] = T::dot2(lo, pp[h], acc[h][2 * k]);
-              acc[h][2 * k + 1] = T::dot2(hi, pp[h], acc[h][2 * k + 1]);
+              acc[h][2 * k] = T::dot2(lo, pp[sp][h], acc[h][2 * k]);
+              acc[h][2 * k + 1] = T::dot2(hi, pp[sp][h], acc[h][2 * k + 1]);
             }
           }
         }

@@ -234,12 +234,15 @@ extern "C" int mce_argmax_rows(int dtype, const void *logits, int64_t rows, int6
   MCE_REQUIRE(rows >= 0 && cols >= 1 && row_stride >= cols, "mce_argmax_rows: bad shape");
   if (rows == 0) return MCE_OK;
   MCE_REQUIRE(logits && out, "mce_argmax_rows: null pointer");
-  MCE_REQUIRE(rows < 65536, "mce_argmax_rows: too many rows");
+  // one workgroup per row on grid.x without the split
+  MCE_REQUIRE(rows < ((int64_t)1 << 31), "mce_argmax_rows: too many rows");
   hipStream_t st = (hipStream_t)stream;
   const size_t need = mce_argmax_rows_workspace_size(rows, cols);
   const bool split = aligned16(logits) && row_stride % 8 == 0 && cols >= 8 &&
                      cols < ((int64_t)1 << 31);
   if (split) {
+    // the split puts rows on grid.y
+    MCE_REQUIRE(rows < 65536, "mce_argmax_rows: at most 65535 rows of 16-byte aligned logits");
     if (workspace == nullptr || workspace_bytes < need ||
         (reinterpret_cast<uintptr_t>(workspace) & 7) != 0)
       return set_error(MCE_ERR_WORKSPACE,

@@ -28,20 +28,24 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(
   const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + row * in_stride);
   const u32x4 *wr = reinterpret_cast<const u32x4 *>(w);
   u32x4 v[VPT], wv[VPT];
-  // the weight loads go out with the row loads, ahead of the reduction
+  // Every load is unconditional (chunks past the row re-read its last chunk
+  // and are zeroed by a select): a load under a per-lane condition becomes an
+  // exec-masked branch that waits for the loads before it, which kept one
+  // 16-byte load per wave in flight and halved the bandwidth.  A zeroed chunk
+  // adds fma(0, 0, ss) = ss, so the sum is the one over the row's chunks.
+  // The weight loads go out with the row loads, ahead of the reduction.
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    int idx = lane + i * 64;
-    if (idx < nvec) wv[i] = wr[idx];
+    const int idx = lane + i * 64;
+    wv[i] = wr[idx < nvec ? idx : nvec - 1];
   }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    int idx = lane + i * 64;
-    if (idx < nvec) {
-      v[i] = xr[idx];
-      ss = sumsq8<T>(v[i], ss);
-    }
+    const int idx = lane + i * 64;
+    const u32x4 t = xr[idx < nvec ? idx : nvec - 1];
+    v[i] = idx < nvec ? t : u32x4{0, 0, 0, 0};
+    ss = sumsq8<T>(v[i], ss);
   }
   ss = wave_sum(ss);
   const float inv = rms_inv(ss, hidden, eps);

@@ -41,4 +41,4 @@ int cu_count() {
 
 extern "C" const char *mce_last_error(void) { return mce::g_last_error; }
 
-extern "C" int mce_abi_version(void) { return 100; }
+extern "C" int mce_abi_version(void) { return MCE_ABI_VERSION; }

@@ -55,8 +55,17 @@ namespace mce {
 
 constexpr int PF_HD = 128;
 constexpr int PF_BN = 32;
-constexpr int KS_PITCH = PF_HD + 8;  // halfs per K row in LDS (272 B)
-constexpr int VS_PITCH = PF_HD + 32;  // halfs per V row in LDS (320 B)
+// A 32-key K or V tile in LDS: 8 blocks of 4 key rows of 256 bytes (no row
+// padding: one direct-to-LDS load instruction, 64 lanes x 16 bytes, fills one
+// block), the blocks PF_BLK bytes apart so that consecutive blocks start 64
+// bytes further along the banks.  Inside a block the 16-byte chunks of row a
+// (0..3) are permuted: chunk c of a K row sits at position c ^ a, of a V row
+// at c ^ 4a (whole 64-byte segments).  Then the K fragment reads (16 lanes:
+// 16 keys x one chunk) and the transposing V reads (32 lanes: 4 rows x 64
+// bytes) touch every bank once, and each lane's read offsets differ from one
+// another by constants (immediate offsets).
+constexpr int PF_BLK = 1088;         // bytes between 4-row blocks
+constexpr int PF_TILE = 8 * PF_BLK;  // bytes of one K or V tile
 constexpr float RESCALE_TAU = 8.0f;  // log2 headroom before raising the max
 // Buffer descriptor word 3 for raw (stride 0) dword loads on gfx9-family
 // parts: data format 32, no swizzle, range-checked against num_records.
@@ -74,6 +83,25 @@ __device__ __forceinline__ floatx16 mfma32(u32x4 a, u32x4 b, floatx16 c) {
 }
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer load of 16 bytes per lane straight into LDS: lane l's bytes land at
+// LDS address m0 + 16 l (m0 wave-uniform).  Written as inline asm rather than
+// the builtin: the compiler orders the builtin's LDS write before every later
+// read of the same LDS array with a vmcnt wait, which would stall the step's
+// fragment reads (of the other buffer) until the load landed.  The waits the
+// kernel needs are explicit (s_waitcnt vmcnt before the publishing barrier);
+// loads the compiler does not see only make its own vmcnt waits stricter.
+__device__ __forceinline__ void buffer_load_lds16(i32x4 rsrc, int voff, int soff, unsigned m0) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(voff), "s"(rsrc), "s"(soff),
+               "{m0}"(m0));
+}
+
+// Raw buffer descriptor (stride 0, range-checked against `bytes`).
+__device__ inline i32x4 buffer_rsrc(const void *base, int bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  return i32x4{(int)(uint32_t)p, (int)(uint32_t)(p >> 32) & 0xffff, bytes, BUF_RSRC_WORD3};
+}
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane s supplies the address
 // of 4 consecutive 16-bit values (row s / 4, columns 4 (s % 4) .. +3 of a
@@ -167,11 +195,9 @@ __global__ __launch_bounds__(NRB * KSPLIT * 64) __attribute__((amdgpu_waves_per_
 void prefill_causal_kernel(PrefillArgs a) {
   static_assert(!SPLITK || (PAGED && KSPLIT == 2), "key parts: paged mode, two key streams");
   constexpr int BM = 32 * NRB;
-  constexpr int NT = NRB * 64;                     // threads per key stream
-  constexpr int K_PIECES = PF_BN * PF_HD / 8;      // 16-byte pieces per K tile
-  constexpr int KP = K_PIECES / NT;               // per thread, K and V alike
-  static_assert(KP * NT == K_PIECES, "whole tiles per thread");
-  constexpr int KS_SIZE = PF_BN * KS_PITCH, VS_SIZE = PF_BN * VS_PITCH;
+  // blocks of every K and V tile each wave of a key stream stages
+  constexpr int KP = 8 / NRB;
+  static_assert(KP * NRB == 8, "whole tiles per key stream");
   // Epilogue (reuses the tile buffers): exchanged O halves and (m, l) of the
   // two key streams, then each wave's finished 32 rows x OUT_DIMS before the
   // row-contiguous stores (pitch OUT_DIMS + 8 halfs: 16-byte aligned rows).
@@ -180,12 +206,12 @@ void prefill_causal_kernel(PrefillArgs a) {
   constexpr int XCH_FLOATS = KSPLIT == 2 ? 2 * NRB * 32 * 64 : 0;
   constexpr int ML_FLOATS = KSPLIT == 2 ? 2 * NRB * 2 * 64 : 0;
   constexpr int EPI_HALFS = 2 * (XCH_FLOATS + ML_FLOATS) + NRB * KSPLIT * 32 * YS_PITCH;
-  // [key stream][double buffer] K and V tiles, then the epilogue buffers
-  constexpr int TILE_HALFS = 2 * KSPLIT * (KS_SIZE + VS_SIZE);
+  // [key stream][double buffer] K tiles, then V tiles; the epilogue reuses them
+  constexpr int TILE_HALFS = 2 * KSPLIT * 2 * PF_TILE / 2;
   constexpr int LDS_HALFS = TILE_HALFS > EPI_HALFS ? TILE_HALFS : EPI_HALFS;
   __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALFS];
-  uint16_t *const Ks = lds;
-  uint16_t *const Vs = lds + 2 * KSPLIT * KS_SIZE;
+  char *const Ks = reinterpret_cast<char *>(lds);
+  char *const Vs = Ks + 2 * KSPLIT * PF_TILE;
 
   // workgroup -> (item, batch, kv head); kv head fastest so that the
   // workgroups of one kv head share an XCD (and its L2) when Hkv B == 8.
@@ -209,10 +235,9 @@ void prefill_causal_kernel(PrefillArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rb = w % NRB, kh = w / NRB;
-  const int tid_h = tid - kh * NT;  // thread index within the key stream
   const int hf = lane >> 5, r32 = lane & 31;
-  uint16_t *const ks_h = Ks + kh * 2 * KS_SIZE;
-  uint16_t *const vs_h = Vs + kh * 2 * VS_SIZE;
+  char *const ks_h = Ks + kh * 2 * PF_TILE;  // this stream's K tiles (2 buffers)
+  char *const vs_h = Vs + kh * 2 * PF_TILE;
 
   const int64_t q_row_stride = (int64_t)a.Hq * PF_HD;
   const int kv_row = a.Hkv * PF_HD;  // elements between consecutive keys
@@ -231,91 +256,95 @@ void prefill_causal_kernel(PrefillArgs a) {
   }
   const float c = a.scale_log2;
 
-  // Per-thread staging assignments within a key stream (fixed for the kernel):
-  // piece pc -> key pc / 16, 16-byte column pc % 16 (16 lanes per key row),
-  // the same for K and V.
-  // Loads are unconditional buffer loads (straight-line code keeps the
-  // compiler's vmcnt accounting exact, so staging waits only for the tile it
-  // stores) with loop-invariant per-thread offsets; the hardware range check
-  // of the buffer descriptor returns zeros for keys at or past the sequence
-  // end (the descriptor spans this (batch, kv head)'s rows up to key S).
+  // Staging, straight from global memory into LDS (buffer loads with the LDS
+  // destination, 16 bytes per lane): wave rb of key stream kh fills blocks
+  // KP rb .. KP rb + KP - 1 of every K and V tile of its stream.  Lane l
+  // fetches row a = l / 16 of the block, chunk (l % 16) ^ a of a K row or
+  // (l % 16) ^ 4a of a V row, so that the instruction's 64 x 16 bytes land in
+  // the permuted block layout; each 16-lane group reads one whole 256-byte
+  // row.  No registers hold staged data and no LDS write instructions issue;
+  // each wave waits for its own loads (vmcnt) before the barrier that
+  // publishes the tile.
+  // Unconditional buffer loads: the hardware range check of the descriptor
+  // returns zeros for keys at or past the sequence end (the descriptor spans
+  // this (batch, kv head)'s rows up to key S).
   // (paged: the descriptor spans the whole pool; keys past the sequence end
   // are clamped to its last key, which the causal mask hides)
   const int kv_bytes = PAGED ? (int)(a.cache_bytes - g * PF_HD * 2) : (S * kv_row - g * PF_HD) * 2;
-  const __amdgpu_buffer_rsrc_t krsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void *)kbase, (short)0, kv_bytes, BUF_RSRC_WORD3);
-  const __amdgpu_buffer_rsrc_t vrsrc =
-      __builtin_amdgcn_make_buffer_rsrc((void *)vbase, (short)0, kv_bytes, BUF_RSRC_WORD3);
-  int kv_voff[KP];
+  const i32x4 krsrc = buffer_rsrc(kbase, kv_bytes), vrsrc = buffer_rsrc(vbase, kv_bytes);
+  const int la = lane >> 4, lp = lane & 15;
+  const int ck = lp ^ la, cv = lp ^ (4 * la);  // chunk this lane fetches (K / V)
+  // contiguous mode: byte offset of this lane's piece of block j inside a tile
+  int voff_k[KP], voff_v[KP];
 #pragma unroll
-  for (int it = 0; it < KP; ++it) {
-    const int pc = tid_h + it * NT;
-    kv_voff[it] = PAGED ? (pc & 15) * 8 * 2 : ((pc >> 4) * kv_row + (pc & 15) * 8) * 2;
+  for (int j = 0; j < KP; ++j) {
+    const int key = 4 * (KP * rb + j) + la;
+    voff_k[j] = PAGED ? ck * 16 : (key * kv_row + ck * 8) * 2;
+    voff_v[j] = PAGED ? cv * 16 : (key * kv_row + cv * 8) * 2;
   }
-  // paged mode: byte offset in the pool of piece it of stream tile u (the
-  // pieces of a thread share their column and lie NT / 16 keys apart)
+  // paged mode: byte offset in the pool of the row of key `key`
   const int bsm = (1 << a.bs_log2) - 1;
-  const int pkey = tid_h >> 4, pcol = (tid_h & 15) * 16;
-  auto paged_off = [&](int u, int it) {
-    const int key = min((tb + KSPLIT * u + kh) * PF_BN + pkey + it * (NT / 16), key_S - 1);
-    return bt_lds[key >> a.bs_log2] + (key & bsm) * kv_row * 2 + pcol;
+  auto page_row = [&](int key) {
+    key = min(key, key_S - 1);
+    return bt_lds[key >> a.bs_log2] + (key & bsm) * kv_row * 2;
   };
   // stream index u of this key stream <-> key tile KSPLIT u + kh
   // (wave-uniform, passed as the scalar offset of the buffer loads)
   auto tile_off = [&](int u) {
     return __builtin_amdgcn_readfirstlane((KSPLIT * u + kh) * PF_BN * kv_row * 2);
   };
-  using KRegs = u32x4[KP];
-  using VRegs = u32x4[KP];
-  // One register set of staged tiles in flight (each tile fetched one step
-  // before it is staged): a second set, fetching two steps ahead, measured
-  // 2-2.5% slower in the contiguous mode and 4-10% in the paged mode (whose
-  // page-offset arithmetic then spilled).
-  constexpr int AHEAD = 3;  // the K tile fetched at step u is u + AHEAD
-  KRegs kreg;
-  VRegs vreg;
-  auto load_k = [&](KRegs &dst, int u) {
+  // LDS address (m0) of this wave's first block in K / V buffer 0
+  const unsigned lds0 = (unsigned)reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) char *)reinterpret_cast<char *>(lds));
+  const unsigned k_m0 = __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(ks_h - Ks) + KP * rb * PF_BLK);
+  const unsigned v_m0 = __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(vs_h - Ks) + KP * rb * PF_BLK);
+  // K and V tiles u of this stream into buffer u % 2
+  auto stage_k = [&](int u) {
+    const unsigned m0 = k_m0 + (u & 1) * PF_TILE;
     if constexpr (PAGED) {
 #pragma unroll
-      for (int it = 0; it < KP; ++it)
-        dst[it] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(krsrc, paged_off(u, it), 0, 0));
+      for (int j = 0; j < KP; ++j)
+        buffer_load_lds16(
+            krsrc, page_row((tb + KSPLIT * u + kh) * PF_BN + 4 * (KP * rb + j) + la) + voff_k[j], 0,
+            m0 + j * PF_BLK);
     } else {
       const int off = tile_off(u);
 #pragma unroll
-      for (int it = 0; it < KP; ++it)
-        dst[it] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(krsrc, kv_voff[it], off, 0));
+      for (int j = 0; j < KP; ++j) buffer_load_lds16(krsrc, voff_k[j], off, m0 + j * PF_BLK);
     }
   };
-  auto load_v = [&](VRegs &dst, int u) {
+  auto stage_v = [&](int u) {
+    const unsigned m0 = v_m0 + (u & 1) * PF_TILE;
     if constexpr (PAGED) {
 #pragma unroll
-      for (int it = 0; it < KP; ++it)
-        dst[it] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrsrc, paged_off(u, it), 0, 0));
+      for (int j = 0; j < KP; ++j)
+        buffer_load_lds16(
+            vrsrc, page_row((tb + KSPLIT * u + kh) * PF_BN + 4 * (KP * rb + j) + la) + voff_v[j], 0,
+            m0 + j * PF_BLK);
     } else {
       const int off = tile_off(u);
 #pragma unroll
-      for (int it = 0; it < KP; ++it)
-        dst[it] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(vrsrc, kv_voff[it], off, 0));
+      for (int j = 0; j < KP; ++j) buffer_load_lds16(vrsrc, voff_v[j], off, m0 + j * PF_BLK);
     }
   };
-  auto store_k = [&](const KRegs &src, uint16_t *ks) {
+  // this wave's staging loads have landed in LDS (s_waitcnt vmcnt(0))
+  auto staged = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
+  // Fragment read offsets inside a tile.  K (scores): lane (r32, hf) reads
+  // chunk 2 i + hf of key r32, at 64 (i / 2) + kfo[i % 2].  V^T (P V): lane
+  // 16 q + s of group q reads dims 32 dt + 16 (q & 1) + 4 (s & 3) .. + 3 of
+  // key rows 16 kk + 4 (q >> 1) + s / 4 and + 8, at vfo[dt] + (4 kk) PF_BLK
+  // and + (4 kk + 2) PF_BLK.
+  int kfo[2], vfo[4];
+  {
+    const int kb = r32 >> 2, ka = r32 & 3;
 #pragma unroll
-    for (int it = 0; it < KP; ++it) {
-      const int pc = tid_h + it * NT;
-      *reinterpret_cast<u32x4 *>(&ks[(pc >> 4) * KS_PITCH + (pc & 15) * 8]) = src[it];
-    }
-  };
-  auto store_v = [&](const VRegs &src, uint16_t *vs) {
+    for (int t = 0; t < 2; ++t) kfo[t] = kb * PF_BLK + ka * 256 + 16 * ((2 * t + hf) ^ ka);
+    const int q4 = lane >> 4, s16 = lane & 15, va = s16 >> 2;
 #pragma unroll
-    for (int it = 0; it < KP; ++it) {
-      const int pc = tid_h + it * NT;
-      *reinterpret_cast<u32x4 *>(&vs[(pc >> 4) * VS_PITCH + (pc & 15) * 8]) = src[it];
-    }
-  };
+    for (int dt = 0; dt < 4; ++dt)
+      vfo[dt] = (q4 >> 1) * PF_BLK + va * 256 +
+                16 * (4 * (dt ^ va) + 2 * (q4 & 1) + ((s16 >> 1) & 1)) + 8 * (s16 & 1);
+  }
 
   const int rows_total = S * G;
   const int item = a.n_items - 1 - item_rank;  // heaviest items first
@@ -351,8 +380,7 @@ void prefill_causal_kernel(PrefillArgs a) {
   constexpr bool PRESCALED = T::code == MCE_F16;
   //
   // Q, K_0, K_1 and V_0 are fetched together (one memory round trip before
-  // the first tile instead of one per dependent stage); the two register
-  // sets follow once K_0 is staged.
+  // the first tile instead of one per dependent stage).
   u32x4 qreg[8];
   {
     const uint16_t *qp = a.q + ((int64_t)b * S + (row_ok ? qi : 0)) * q_row_stride +
@@ -360,11 +388,9 @@ void prefill_causal_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) qreg[i] = *reinterpret_cast<const u32x4 *>(qp + 16 * i);
   }
-  KRegs k0, k1;
-  VRegs v0;
-  load_k(k0, 0);
-  load_k(k1, 1);
-  load_v(v0, 0);
+  stage_k(0);
+  stage_k(1);
+  stage_v(0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -381,13 +407,12 @@ void prefill_causal_kernel(PrefillArgs a) {
   }
 
   // S^T of one 32-key tile, accumulators starting at `init`.
-  auto scores = [&](const uint16_t *ks, float init, floatx16 &st) {
+  auto scores = [&](const char *kt, float init, floatx16 &st) {
 #pragma unroll
     for (int e = 0; e < 16; ++e) st[e] = init;
-    const uint16_t *kp = &ks[r32 * KS_PITCH + 8 * hf];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-      st = mfma32<T>(*reinterpret_cast<const u32x4 *>(kp + 16 * i), qreg[i], st);
+      st = mfma32<T>(*reinterpret_cast<const u32x4 *>(kt + kfo[i & 1] + 64 * (i >> 1)), qreg[i], st);
   };
 
   // Online-softmax state of this lane's row: running max m_run (log2 units;
@@ -451,67 +476,60 @@ void prefill_causal_kernel(PrefillArgs a) {
     thr = grow ? RESCALE_TAU : thr;
   };
 
-  // Prologue (per key stream): K_0 staged and scored (prepared in s_a); K_1
-  // and V_0 staged into the second
-  // / first buffers; (K_2, V_1) fetched into the staging registers (indices
-  // are stream indices u).
-  store_k(k0, ks_h);
+  // Prologue (per key stream): K_0, K_1 and V_0 staged (indices are stream
+  // indices u), K_0 scored (prepared in s_a).
+  staged();
   lds_barrier();
-  load_k(kreg, 2);
-  load_v(vreg, 1);
-  __builtin_amdgcn_sched_barrier(0);
   {
     scores(ks_h, 0.f, s_a);
     prep(s_a, tb + kh);
     const float mx = rowmax(s_a);
     if (__ballot(mx > thr) != 0) rescale(mx, s_a);
   }
-  store_k(k1, ks_h + KS_SIZE);
-  store_v(v0, vs_h);
 
-  // Iteration u (key tile kt = KSPLIT u + kh), one straight-line block:
+  // Iteration u (key tile kt = KSPLIT u + kh), one straight-line block after
+  // the barrier that publishes K_{u+1} and V_u:
+  //   K_{u+2} / V_{u+1} are staged (direct-to-LDS loads) into the buffers
+  //      that iteration u - 1 finished reading; they have the whole
+  //      iteration to land;
   //   A: scores of tile u + 1 (K in buffer (u+1)%2, accumulators starting at
   //      -m_run) on the matrix cores while the exp2 / convert / row-sum work
   //      of tile u runs on the VALU;
-  //   K_{u+2} / V_{u+1} are staged from the staging registers into the
-  //      buffers that iteration u - 1 finished reading;
   //   B: P V of tile u (V^T in buffer u%2) while tile u + 1 is masked (DIAG)
-  //      and max-reduced; then K_{u+3} / V_{u+2} are fetched into the
-  //      staging registers;
+  //      and max-reduced;
   // rows whose max grew are rescaled after the block.  The mask is applied
   // only by the DIAG form (tiles that reach the diagonal or the sequence end),
   // and waves past their last tile only stage (stage_only), so the three
   // loops below keep every step free of branches.  Barriers match by count:
   // every wave runs the same (even) number of iterations.  Staging is
-  // unconditional, so the loop carries the staging registers without copies (a
-  // copy of a pending load would wait for every load in flight); tiles past
-  // the end are zero-filled and written to buffers nobody reads again.
+  // unconditional; tiles past the end are zero-filled (or clamped) and land
+  // in buffers nobody reads again.
   auto step = [&](const int u, floatx16 &s_cur, floatx16 &s_nxt, auto diag) {
     constexpr bool DIAG = decltype(diag)::value;
+    staged();
     lds_barrier();
+    stage_k(u + 2);
+    stage_v(u + 1);
     // LLVM's built-in MFMA / LDS-read interleaving strategy for the step's
     // block (same instructions, another order): 1-2% faster at every shape
     // measured, with fewer registers.
     __builtin_amdgcn_iglp_opt(0);
     const int kt = tb + KSPLIT * u + kh;  // key tile
-    const uint16_t *kp = &ks_h[((u + 1) & 1) * KS_SIZE + r32 * KS_PITCH + 8 * hf];
-    // V^T fragment (dt, kk): lane l = 16 q + s of group q takes dims 32 dt +
-    // 16 (q & 1) + 0..15 and keys 16 kk + 4 (q >> 1) + 0..3 (first read) and
-    // + 8 (second); it points at key ... + s / 4, dims ... + 4 (s % 4).
-    const int q4 = lane >> 4, s16 = lane & 15;
-    const uint16_t *vp = &vs_h[(u & 1) * VS_SIZE + (4 * (q4 >> 1) + (s16 >> 2)) * VS_PITCH +
-                               16 * (q4 & 1) + 4 * (s16 & 3)];
+    const char *kb = ks_h + ((u + 1) & 1) * PF_TILE;
+    const char *vb = vs_h + (u & 1) * PF_TILE;
     u32x4 kf[8];
     u32x4 vf[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) kf[i] = *reinterpret_cast<const u32x4 *>(kp + 16 * i);
+    for (int i = 0; i < 8; ++i)
+      kf[i] = *reinterpret_cast<const u32x4 *>(kb + kfo[i & 1] + 64 * (i >> 1));
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk)
       {
-        const u32x2 lo = ds_read_tr16(vp + 16 * kk * VS_PITCH + 32 * dt);
-        const u32x2 hi = ds_read_tr16(vp + (16 * kk + 8) * VS_PITCH + 32 * dt);
+        const u32x2 lo = ds_read_tr16(reinterpret_cast<const uint16_t *>(vb + vfo[dt] + 4 * kk * PF_BLK));
+        const u32x2 hi =
+            ds_read_tr16(reinterpret_cast<const uint16_t *>(vb + vfo[dt] + (4 * kk + 2) * PF_BLK));
         vf[dt * 2 + kk] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
     // ---- A
@@ -527,8 +545,6 @@ void prefill_causal_kernel(PrefillArgs a) {
       l_i = T::dot2(pp, ones, l_i);
       pk[e2 >> 2][e2 & 3] = pp;
     }
-    store_k(kreg, ks_h + (u & 1) * KS_SIZE);
-    store_v(vreg, vs_h + ((u + 1) & 1) * VS_SIZE);
     // ---- B
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
@@ -545,16 +561,13 @@ void prefill_causal_kernel(PrefillArgs a) {
         if (8 * (e >> 2) + (e & 3) > l2) s_nxt[e] = -INFINITY;
     }
     const float mx = rowmax(s_nxt);
-    load_k(kreg, u + AHEAD);
-    load_v(vreg, u + AHEAD - 1);
     if (__builtin_expect(__ballot(mx > thr) != 0, 0)) rescale(mx, s_nxt);
   };
   auto stage_only = [&](const int u) {
+    staged();
     lds_barrier();
-    store_k(kreg, ks_h + (u & 1) * KS_SIZE);
-    store_v(vreg, vs_h + ((u + 1) & 1) * VS_SIZE);
-    load_k(kreg, u + AHEAD);
-    load_v(vreg, u + AHEAD - 1);
+    stage_k(u + 2);
+    stage_v(u + 1);
   };
   // step u needs the mask from u_first on (its next tile KSPLIT (u+1) + kh
   // reaches n_full); tile KSPLIT u + kh is past this wave's rows from u_end on
@@ -585,7 +598,8 @@ void prefill_causal_kernel(PrefillArgs a) {
   // (m, l), from LDS (16-byte lane-major records, conflict-free).  The
   // finished tile goes through LDS once more so that every store writes whole
   // rows: OUT_DIMS * 2 bytes of a row by consecutive lanes, 16 bytes each.
-  lds_barrier();  // every wave is done with the K / V^T tiles
+  staged();       // the last staging loads have landed (the epilogue reuses
+  lds_barrier();  // the tile buffers); every wave is done with the K / V^T tiles
   float *const xo = reinterpret_cast<float *>(lds);  // [kh][rb][8][64 lanes][4]
   float *const xm = xo + XCH_FLOATS;                 // [kh][rb][2][64 lanes]
   uint16_t *const ys = reinterpret_cast<uint16_t *>(xm + ML_FLOATS) + w * 32 * YS_PITCH;

@@ -6,6 +6,7 @@ pure size query), so it runs on a machine without a GPU.
 """
 import ctypes
 import os
+import re
 
 import pytest
 import torch
@@ -44,7 +45,10 @@ def test_single_hip_runtime_mapped(lib):
 
 
 def test_version(lib):
-    assert lib.mce_abi_version() >= 100
+    # exact: the ctypes signatures in _lib are those of this version
+    assert lib.mce_abi_version() == _lib.MCE_ABI_VERSION == 101
+    hdr = open(_lib.HEADER_PATH).read()
+    assert re.search(r"#define MCE_ABI_VERSION 101\b", hdr)
 
 
 def _err(lib):
@@ -234,6 +238,13 @@ def test_decode_loop_entry_points_validate(lib):
     # aligned rows are split: the workspace is required
     assert f(0, one, 8, 128256, 128256, one, None, 0, None) == _lib.MCE_ERR_WORKSPACE
     assert f(0, one, 8, 128256, 128256, one, one, 8, None) == _lib.MCE_ERR_WORKSPACE
+    # the split (rows on grid.y) takes at most 65535 rows; the one-workgroup-per-row
+    # path (unaligned rows: rows on grid.x) is not limited to that
+    assert f(0, one, 70000, 128, 128, one, one, 1 << 30, None) == _lib.MCE_ERR_INVALID
+    assert "65535" in _err(lib)
+    odd = ctypes.c_void_p(18)  # 2-byte aligned only: the unsplit path
+    assert f(0, odd, 1 << 31, 128, 129, one, None, 0, None) == _lib.MCE_ERR_INVALID
+    assert "too many rows" in _err(lib)
     g = lib.mce_decode_advance
     assert g(None, None, None, None, None, None, None, 4, 8, 16, 0, None) == _lib.MCE_ERR_INVALID
     one = ctypes.c_void_p(16)  # non-null, never dereferenced: validation fails first

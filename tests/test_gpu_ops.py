@@ -486,6 +486,17 @@ def test_argmax_rows_matches_torch(dev, dtype, rows, cols, stride):
     assert got.tolist() == argmax_rows_ref(x.float().numpy()).tolist()
 
 
+def test_argmax_rows_many_unaligned_rows(dev):
+    """Rows whose stride is not a multiple of 8 take one workgroup per row on
+    grid.x, so row counts past the split path's 65535 (grid.y) are accepted
+    and equal torch.argmax."""
+    from mycustomcudaengine_amd.ops import argmax_rows
+    g = gen(171)
+    x = (torch.randn(70001, 9, generator=g) * 4).half()
+    got = argmax_rows(x.to(dev)).cpu()
+    assert got.tolist() == torch.argmax(x.float(), dim=-1).tolist()
+
+
 def test_decode_advance_matches_oracle_and_replays(dev):
     """Device-side step preparation equals the oracle step after step
     (positions, context lengths, slots from the zero-padded table, -1 past its
