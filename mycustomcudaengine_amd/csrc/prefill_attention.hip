@@ -49,6 +49,7 @@
 // prefill_merge_kernel combines by log-sum-exp.
 #include "mce_common.h"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace mce {
@@ -215,21 +216,26 @@ void prefill_causal_kernel(PrefillArgs a) {
   constexpr int XCH_FLOATS = KSPLIT == 2 ? 2 * NRB * 32 * 64 : 0;
   constexpr int ML_FLOATS = KSPLIT == 2 ? 2 * NRB * 2 * 64 : 0;
   constexpr int EPI_HALFS = 2 * (XCH_FLOATS + ML_FLOATS) + NRB * KSPLIT * 32 * YS_PITCH;
-  // [key stream][double buffer] K tiles, then V tiles; the epilogue reuses them
-  constexpr int TILE_HALFS = 2 * KSPLIT * 2 * TILE / 2;
+  // [key stream][double buffer] K tiles, then V tiles, then (two key streams)
+  // the item's Q rows (NRB 32-row groups in the K tile layout); the epilogue
+  // reuses them all.  One-stream launches load Q straight into registers:
+  // their LDS has to leave room for two workgroups per CU, which overlap one
+  // workgroup's start with the other's steps.
+  constexpr bool Q_LDS = KSPLIT == 2;
+  constexpr int TILE_HALFS = (2 * KSPLIT * 2 * TILE + (Q_LDS ? NRB * PF_TILE : 0)) / 2;
   constexpr int LDS_HALFS = TILE_HALFS > EPI_HALFS ? TILE_HALFS : EPI_HALFS;
   __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALFS];
   char *const Ks = reinterpret_cast<char *>(lds);
   char *const Vs = Ks + 2 * KSPLIT * TILE;
+  char *const Qs = Vs + 2 * KSPLIT * TILE;
 
-  // workgroup -> (item, batch, kv head); kv head fastest so that the
+  // workgroup -> (slot, batch, kv head); kv head fastest so that the
   // workgroups of one kv head share an XCD (and its L2) when Hkv B == 8.
   const int id = blockIdx.x;
   const int g = id % a.Hkv;
   const int b = (id / a.Hkv) % a.B;
   const int rest = id / (a.Hkv * a.B);
   const int part = SPLITK ? rest % a.nsplit : 0;
-  const int item_rank = SPLITK ? rest / a.nsplit : rest;
   int tb = 0;  // first key tile of this workgroup's part (0 without SPLITK)
   const int G = a.G, S = a.S;
   // keys of this sequence and the position of its first query row
@@ -237,7 +243,7 @@ void prefill_causal_kernel(PrefillArgs a) {
   const int p0 = key_S - S;
   // SPLITK: parts of this item (from its real key range); workgroups of
   // parts past them have nothing to do
-  const int n_parts = SPLITK ? prefill_parts(a, key_S, a.n_items - 1 - item_rank, BM) : 1;
+  const int n_parts = SPLITK ? prefill_parts(a, key_S, a.n_items - 1 - rest / a.nsplit, BM) : 1;
   if (SPLITK && part >= n_parts) return;
   __shared__ int bt_lds[PAGED ? PF_MAX_BLOCKS : 1];
 
@@ -249,6 +255,8 @@ void prefill_causal_kernel(PrefillArgs a) {
   char *const vs_h = Vs + kh * 2 * TILE;
 
   const int64_t q_row_stride = (int64_t)a.Hq * PF_HD;
+  // this sequence's queries (rows of Hq heads, 256 bytes each; < 2^31 bytes)
+  const i32x4 qrsrc = buffer_rsrc(a.q + (int64_t)b * S * q_row_stride, S * a.Hq * PF_HD * 2);
   const int kv_row = a.Hkv * PF_HD;  // elements between consecutive keys
   const uint16_t *kbase = PAGED ? a.k + (int64_t)g * PF_HD : a.k + ((int64_t)b * S * a.Hkv + g) * PF_HD;
   const uint16_t *vbase = PAGED ? a.v + (int64_t)g * PF_HD : a.v + ((int64_t)b * S * a.Hkv + g) * PF_HD;
@@ -309,7 +317,11 @@ void prefill_causal_kernel(PrefillArgs a) {
       (__attribute__((address_space(3))) char *)reinterpret_cast<char *>(lds));
   const unsigned k_m0 = __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(ks_h - Ks) + KP * rb * PF_BLK);
   const unsigned v_m0 = __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(vs_h - Ks) + KP * rb * PF_BLK);
-  // K and V tiles u of this stream into buffer u % 2
+  const unsigned q_m0 = __builtin_amdgcn_readfirstlane(lds0 + (unsigned)(Qs - Ks));
+  // K and V tiles u of this stream into buffer u % 2.  The loads are issued
+  // unconditionally, also the last iteration's (never read): a build that
+  // skipped the never-read K load under a branch computed wrong outputs from
+  // the first tiles on, so the staging stays branch-free.
   auto stage_k = [&](int u) {
     const unsigned m0 = k_m0 + (u & 1) * TILE;
 #pragma unroll
@@ -368,400 +380,439 @@ void prefill_causal_kernel(PrefillArgs a) {
   }
 
   const int rows_total = S * G;
-  const int item = a.n_items - 1 - item_rank;  // heaviest items first
-  const int r_item = item * BM;
-  const int r_wave = r_item + 32 * rb;
-  const int row = r_wave + r32;                 // this lane's row
-  const int qi = row / G, h = g * G + (row - qi * G);
-  const int pos = p0 + qi;                      // its position among the keys
-  const bool row_ok = row < rows_total;
-  const int wave_min_pos = p0 + r_wave / G;
-  const int item_max_pos = p0 + min(S - 1, (r_item + BM - 1) / G);
-  const int n_ktiles = item_max_pos / BN + 1;  // key tiles of the item
-  // SPLITK: this part's key tiles [tb, te)
-  if constexpr (SPLITK) tb = (int)((int64_t)part * n_ktiles / n_parts);
-  const int te = SPLITK ? (int)((int64_t)(part + 1) * n_ktiles / n_parts) : n_ktiles;
-  // iterations per key stream, rounded up to even for the ping-pong unroll
-  const int n_iter = ((te - tb + KSPLIT - 1) / KSPLIT + 1) / 2 * 2;
-  // key tiles this wave's rows need (none for a block of padding rows)
-  const int n_wtiles =
-      r_wave < rows_total ? (p0 + min(S - 1, min(r_wave + 31, rows_total - 1) / G)) / BN + 1 : 0;
-  // tiles [0, n_full) need no mask for this wave: every key <= its first
-  // position and < key_S (SPLITK: and below the part's end, so that no key of
-  // the next part is ever scored into this part's state)
-  const int n_full = SPLITK ? min(min((wave_min_pos + 1) / BN, key_S / BN), te)
-                            : min((wave_min_pos + 1) / BN, key_S / BN);
-  // masked tiles: key offset limit + n0
-  const int lim = (SPLITK ? min(min(pos, key_S - 1), te * BN - 1) : min(pos, key_S - 1)) - 4 * hf;
+  // Items of this workgroup.  Without the key split the launch has P
+  // workgroups per (sequence, kv head), at most one per CU, and workgroup j
+  // takes item ranks j and 2 P - 1 - j (ranks count from the heaviest item):
+  // the lightest items run behind medium ones on the same CU instead of as a
+  // second round of workgroups, which paid a start-up and a drain each.
+  // (two-stream launches only: the one-stream launches have a workgroup per
+  // item, several per CU, and the key split one per part)
+  constexpr int MAX_MINE = KSPLIT == 2 && !SPLITK ? 2 : 1;
+  const int P = MAX_MINE == 1 ? 1 : (int)(gridDim.x / (unsigned)(a.Hkv * a.B));
+  const int n_mine = MAX_MINE == 2 && 2 * P - 1 - rest < a.n_items ? 2 : 1;
+  for (int mi = 0; mi < MAX_MINE && mi < n_mine; ++mi) {
+    const int item_rank = SPLITK ? rest / a.nsplit : (mi == 0 ? rest : 2 * P - 1 - rest);
+    if (mi > 0) lds_barrier();  // every wave is done with the previous item's LDS
+    const int item = a.n_items - 1 - item_rank;  // heaviest items first
+    const int r_item = item * BM;
+    const int r_wave = r_item + 32 * rb;
+    const int row = r_wave + r32;                 // this lane's row
+    const int qi = row / G;
+    const int pos = p0 + qi;                      // its position among the keys
+    const bool row_ok = row < rows_total;
+    const int wave_min_pos = p0 + r_wave / G;
+    const int item_max_pos = p0 + min(S - 1, (r_item + BM - 1) / G);
+    const int n_ktiles = item_max_pos / BN + 1;  // key tiles of the item
+    // SPLITK: this part's key tiles [tb, te)
+    if constexpr (SPLITK) tb = (int)((int64_t)part * n_ktiles / n_parts);
+    const int te = SPLITK ? (int)((int64_t)(part + 1) * n_ktiles / n_parts) : n_ktiles;
+    // iterations per key stream, rounded up to even for the ping-pong unroll
+    const int n_iter = ((te - tb + KSPLIT - 1) / KSPLIT + 1) / 2 * 2;
+    // key tiles this wave's rows need (none for a block of padding rows)
+    const int n_wtiles =
+        r_wave < rows_total ? (p0 + min(S - 1, min(r_wave + 31, rows_total - 1) / G)) / BN + 1 : 0;
+    // tiles [0, n_full) need no mask for this wave: every key <= its first
+    // position and < key_S (SPLITK: and below the part's end, so that no key of
+    // the next part is ever scored into this part's state)
+    const int n_full = SPLITK ? min(min((wave_min_pos + 1) / BN, key_S / BN), te)
+                              : min((wave_min_pos + 1) / BN, key_S / BN);
+    // masked tiles: key offset limit + n0
+    const int lim = (SPLITK ? min(min(pos, key_S - 1), te * BN - 1) : min(pos, key_S - 1)) - 4 * hf;
 
-  // Q^T as MFMA B operand: lane supplies Q[pos, h][16 i + 8 hf + j], for fp16
-  // pre-scaled by c (so the accumulators come out in log2 units); bf16 keeps
-  // Q exact (its 8-bit mantissa would round c Q too coarsely) and scales the
-  // scores instead (PRESCALED false).
-  constexpr bool PRESCALED = T::code == MCE_F16;
-  //
-  // Q, K_0, K_1 and V_0 are fetched together (one memory round trip before
-  // the first tile instead of one per dependent stage).
-  u32x4 qreg[8];
-  {
-    const uint16_t *qp = a.q + ((int64_t)b * S + (row_ok ? qi : 0)) * q_row_stride +
-                         (int64_t)(row_ok ? h : 0) * PF_HD + 8 * hf;
+    // Q^T as MFMA B operand: lane supplies Q[pos, h][16 i + 8 hf + j], for fp16
+    // pre-scaled by c (so the accumulators come out in log2 units); bf16 keeps
+    // Q exact (its 8-bit mantissa would round c Q too coarsely) and scales the
+    // scores instead (PRESCALED false).
+    constexpr bool PRESCALED = T::code == MCE_F16;
+    //
+    // Q, K_0, K_1 and V_0 are fetched together (one memory round trip before
+    // the first tile instead of one per dependent stage).  With two key
+    // streams Q comes through LDS like K: whole 256-byte rows per 16-lane
+    // group (the MFMA operand pattern straight from global memory, 32 rows x
+    // 32 bytes per load instruction, keeps the address path busy ~3.5x
+    // longer), loaded once for both streams; wave w fills 4-row blocks
+    // QB w .. QB w + QB - 1 of the item (rows past the end re-read the last
+    // row and are zeroed below).
+    u32x4 qreg[8];
+    if constexpr (Q_LDS) {
+      constexpr int QB = 8 / KSPLIT;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qreg[i] = *reinterpret_cast<const u32x4 *>(qp + 16 * i);
-  }
-  stage_k(0);
-  stage_k(1);
-  stage_v(0);
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const u32x4 x = row_ok ? qreg[i] : u32x4{0, 0, 0, 0};
-    if constexpr (PRESCALED) {
-      const half8 xh = __builtin_bit_cast(half8, x);
-      half8 y;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) y[j] = (_Float16)((float)xh[j] * c);
-      qreg[i] = __builtin_bit_cast(u32x4, y);
+      for (int j = 0; j < QB; ++j) {
+        const int bq = QB * w + j;
+        const int qr = min(r_item + 4 * bq + la, rows_total - 1);
+        const int qp = qr / G;
+        const int qh = g * G + (qr - qp * G);
+        buffer_load_lds16(qrsrc, (qp * a.Hq + qh) * PF_HD * 2 + ck * 16, 0,
+                          q_m0 + (bq >> 3) * PF_TILE + (bq & 7) * PF_BLK);
+      }
     } else {
-      qreg[i] = x;
+      const int qh = g * G + (row - qi * G);
+      const uint16_t *qp = a.q + ((int64_t)b * S + (row_ok ? qi : 0)) * q_row_stride +
+                           (int64_t)(row_ok ? qh : 0) * PF_HD + 8 * hf;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qreg[i] = *reinterpret_cast<const u32x4 *>(qp + 16 * i);
     }
-  }
-
-  // S^T of one tile (NH 32-key halves), accumulators starting at `init`.
-  using Scores = floatx16[NH];
-  auto scores = [&](const char *kt, float init, Scores &st) {
-#pragma unroll
-    for (int hh = 0; hh < NH; ++hh) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) st[hh][e] = init;
+    stage_k(0);
+    stage_k(1);
+    stage_v(0);
+    staged();
+    lds_barrier();
+    if constexpr (Q_LDS) {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        st[hh] = mfma32<T>(*reinterpret_cast<const u32x4 *>(kt + hh * PF_TILE + kfo[i & 1] + 64 * (i >> 1)),
-                           qreg[i], st[hh]);
+        qreg[i] = *reinterpret_cast<const u32x4 *>(Qs + rb * PF_TILE + kfo[i & 1] + 64 * (i >> 1));
     }
-  };
-
-  // Online-softmax state of this lane's row: running max m_run (log2 units;
-  // 0 until the row has seen an unmasked key), growth threshold thr (-inf
-  // until then, so the first finite tile max sets m_run; RESCALE_TAU after),
-  // l_i = this lane's half of the row sum, O^T in o.
-  float m_run = 0.f, thr = -INFINITY, l_i = 0.f;
-  floatx16 o[4];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
+    for (int i = 0; i < 8; ++i) {
+      const u32x4 x = row_ok ? qreg[i] : u32x4{0, 0, 0, 0};
+      if constexpr (PRESCALED) {
+        const half8 xh = __builtin_bit_cast(half8, x);
+        half8 y;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
-  Scores s_a, s_b;  // ping-pong: scores ready for exp / next accumulator
-  // accumulator start of every tile's scores: -m_run (fp16, pre-scaled Q) or 0
-  floatx16 acc0;
-#pragma unroll
-  for (int e = 0; e < 16; ++e) acc0[e] = 0.f;
-  const uint32_t ones = T::pack_p(1.0f, 1.0f);
-
-  // Scores of key tile kt straight from the MFMA -> exp2 arguments: bf16
-  // scales them here; tiles past the diagonal (or the sequence end) get -inf
-  // on masked keys.
-  auto prep = [&](Scores &s, const int kt) {
-    if constexpr (!PRESCALED) {
-#pragma unroll
-      for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) s[hh][e] = __builtin_fmaf(s[hh][e], c, -m_run);
-    }
-    if (kt >= n_full) {
-#pragma unroll
-      for (int hh = 0; hh < NH; ++hh) {
-        const int l2 = lim - kt * BN - 32 * hh;
-#pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if (8 * (e >> 2) + (e & 3) > l2) s[hh][e] = -INFINITY;
+        // x c rounded to fp16 (as an fma with a +0 addend, one v_fma_mix per
+        // element instead of convert / multiply / convert / pack; only a -0
+        // product becomes +0)
+        for (int j = 0; j < 8; ++j) y[j] = (_Float16)__builtin_fmaf((float)xh[j], c, 0.0f);
+        qreg[i] = __builtin_bit_cast(u32x4, y);
+      } else {
+        qreg[i] = x;
       }
     }
-  };
-  // max over this lane's row (both 32-lane halves of the wave hold it)
-  auto rowmax = [&](const Scores &s) {
-    float mx = -INFINITY;
+
+    // S^T of one tile (NH 32-key halves), accumulators starting at `init`.
+    using Scores = floatx16[NH];
+    auto scores = [&](const char *kt, float init, Scores &st) {
 #pragma unroll
-    for (int hh = 0; hh < NH; ++hh)
+      for (int hh = 0; hh < NH; ++hh) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[hh][e]);
-    return fmaxf(mx, xor32_max(mx));
-  };
-  // Raise the running max of the rows whose tile max exceeds thr: O, l and
-  // the ready scores move to the new max.  Rare after the first tile (growth
-  // beyond 2^TAU in p units).
-  auto rescale = [&](const float mx, Scores &s_ready) {
-    const bool grow = mx > thr;
-    const float d = grow ? mx : 0.f;
-    const float alpha = thr > -INFINITY ? fast_exp2(-d) : 0.f;
-    l_i *= alpha;
+        for (int e = 0; e < 16; ++e) st[hh][e] = init;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          st[hh] = mfma32<T>(*reinterpret_cast<const u32x4 *>(kt + hh * PF_TILE + kfo[i & 1] + 64 * (i >> 1)),
+                             qreg[i], st[hh]);
+      }
+    };
+
+    // Online-softmax state of this lane's row: running max m_run (log2 units;
+    // 0 until the row has seen an unmasked key), growth threshold thr (-inf
+    // until then, so the first finite tile max sets m_run; RESCALE_TAU after),
+    // l_i = this lane's half of the row sum, O^T in o.
+    float m_run = 0.f, thr = -INFINITY, l_i = 0.f;
+    floatx16 o[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+      for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+    Scores s_a, s_b;  // ping-pong: scores ready for exp / next accumulator
+    // accumulator start of every tile's scores: -m_run (fp16, pre-scaled Q) or 0
+    floatx16 acc0;
 #pragma unroll
-    for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) s_ready[hh][e] -= d;
-    m_run += d;
-    if constexpr (PRESCALED) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc0[e] = -m_run;
-    }
-    thr = grow ? RESCALE_TAU : thr;
-  };
+    for (int e = 0; e < 16; ++e) acc0[e] = 0.f;
+    const uint32_t ones = T::pack_p(1.0f, 1.0f);
 
-  // Prologue (per key stream): K_0, K_1 and V_0 staged (indices are stream
-  // indices u), K_0 scored (prepared in s_a).
-  staged();
-  lds_barrier();
-  {
-    scores(ks_h, 0.f, s_a);
-    prep(s_a, tb + kh);
-    const float mx = rowmax(s_a);
-    if (__ballot(mx > thr) != 0) rescale(mx, s_a);
-  }
-
-  // Iteration u (key tile kt = KSPLIT u + kh), one straight-line block after
-  // the barrier that publishes K_{u+1} and V_u:
-  //   K_{u+2} / V_{u+1} are staged (direct-to-LDS loads) into the buffers
-  //      that iteration u - 1 finished reading; they have the whole
-  //      iteration to land;
-  //   A: scores of tile u + 1 (K in buffer (u+1)%2, accumulators starting at
-  //      -m_run) on the matrix cores while the exp2 / convert / row-sum work
-  //      of tile u runs on the VALU;
-  //   B: P V of tile u (V^T in buffer u%2) while tile u + 1 is masked (DIAG)
-  //      and max-reduced;
-  // rows whose max grew are rescaled after the block.  The mask is applied
-  // only by the DIAG form (tiles that reach the diagonal or the sequence end),
-  // and waves past their last tile only stage (stage_only), so the three
-  // loops below keep every step free of branches.  Barriers match by count:
-  // every wave runs the same (even) number of iterations.  Staging is
-  // unconditional; tiles past the end are zero-filled (or clamped) and land
-  // in buffers nobody reads again.
-  auto step = [&](const int u, Scores &s_cur, Scores &s_nxt, auto diag) {
-    constexpr bool DIAG = decltype(diag)::value;
-    staged();
-    lds_barrier();
-    stage_k(u + 2);
-    stage_v(u + 1);
-    // LLVM's built-in MFMA / LDS-read interleaving strategy for the step's
-    // block (same instructions, another order): 1-2% faster at every shape
-    // measured, with fewer registers.
-    __builtin_amdgcn_iglp_opt(0);
-    const int kt = tb + KSPLIT * u + kh;  // key tile
-    const char *kb = ks_h + ((u + 1) & 1) * TILE;
-    const char *vb = vs_h + (u & 1) * TILE;
-    // ---- A: the NH score chains of tile u + 1 on the matrix cores while
-    // tile u's exp2 / convert / row-sum work runs on the VALU
+    // Scores of key tile kt straight from the MFMA -> exp2 arguments: bf16
+    // scales them here; tiles past the diagonal (or the sequence end) get -inf
+    // on masked keys.
+    auto prep = [&](Scores &s, const int kt) {
+      if constexpr (!PRESCALED) {
 #pragma unroll
-    for (int hh = 0; hh < NH; ++hh) {
-      u32x4 kf[8];
+        for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        kf[i] = *reinterpret_cast<const u32x4 *>(kb + hh * PF_TILE + kfo[i & 1] + 64 * (i >> 1));
-      s_nxt[hh] = mfma32<T>(kf[0], qreg[0], acc0);
-#pragma unroll
-      for (int i = 1; i < 8; ++i) s_nxt[hh] = mfma32<T>(kf[i], qreg[i], s_nxt[hh]);
-    }
-    u32x4 pk[NH][2];
-#pragma unroll
-    for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-      for (int e2 = 0; e2 < 8; ++e2) {
-        const float p0 = fast_exp2(s_cur[hh][2 * e2]);
-        const float p1 = fast_exp2(s_cur[hh][2 * e2 + 1]);
-        const uint32_t pp = T::pack_p(p0, p1);
-        l_i = T::dot2(pp, ones, l_i);
-        pk[hh][e2 >> 2][e2 & 3] = pp;
+          for (int e = 0; e < 16; ++e) s[hh][e] = __builtin_fmaf(s[hh][e], c, -m_run);
       }
-    // ---- B: P V of tile u while tile u + 1 is masked and max-reduced
+      if (kt >= n_full) {
 #pragma unroll
-    for (int hh = 0; hh < NH; ++hh) {
-      u32x4 vf[8];
+        for (int hh = 0; hh < NH; ++hh) {
+          const int l2 = lim - kt * BN - 32 * hh;
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const char *vp = vb + hh * PF_TILE + vfo[dt];
-          const u32x2 lo = ds_read_tr16(reinterpret_cast<const uint16_t *>(vp + 4 * kk * PF_BLK));
-          const u32x2 hi = ds_read_tr16(reinterpret_cast<const uint16_t *>(vp + (4 * kk + 2) * PF_BLK));
-          vf[dt * 2 + kk] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          for (int e = 0; e < 16; ++e)
+            if (8 * (e >> 2) + (e & 3) > l2) s[hh][e] = -INFINITY;
         }
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) o[dt] = mfma32<T>(vf[dt * 2 + kk], pk[hh][kk], o[dt]);
-    }
-    if constexpr (!PRESCALED) {
+      }
+    };
+    // max over this lane's row (both 32-lane halves of the wave hold it)
+    auto rowmax = [&](const Scores &s) {
+      float mx = -INFINITY;
 #pragma unroll
       for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) s_nxt[hh][e] = __builtin_fmaf(s_nxt[hh][e], c, -m_run);
+        for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[hh][e]);
+      return fmaxf(mx, xor32_max(mx));
+    };
+    // Raise the running max of the rows whose tile max exceeds thr: O, l and
+    // the ready scores move to the new max.  Rare after the first tile (growth
+    // beyond 2^TAU in p units).
+    auto rescale = [&](const float mx, Scores &s_ready) {
+      const bool grow = mx > thr;
+      const float d = grow ? mx : 0.f;
+      const float alpha = thr > -INFINITY ? fast_exp2(-d) : 0.f;
+      l_i *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dt][e] *= alpha;
+#pragma unroll
+      for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s_ready[hh][e] -= d;
+      m_run += d;
+      if constexpr (PRESCALED) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc0[e] = -m_run;
+      }
+      thr = grow ? RESCALE_TAU : thr;
+    };
+
+    // Prologue (per key stream): K_0, K_1 and V_0 staged above (indices are
+    // stream indices u), K_0 scored (prepared in s_a).
+    {
+      scores(ks_h, 0.f, s_a);
+      prep(s_a, tb + kh);
+      const float mx = rowmax(s_a);
+      if (__ballot(mx > thr) != 0) rescale(mx, s_a);
     }
-    if constexpr (DIAG) {
+
+    // Iteration u (key tile kt = KSPLIT u + kh), one straight-line block after
+    // the barrier that publishes K_{u+1} and V_u:
+    //   K_{u+2} / V_{u+1} are staged (direct-to-LDS loads) into the buffers
+    //      that iteration u - 1 finished reading; they have the whole
+    //      iteration to land;
+    //   A: scores of tile u + 1 (K in buffer (u+1)%2, accumulators starting at
+    //      -m_run) on the matrix cores while the exp2 / convert / row-sum work
+    //      of tile u runs on the VALU;
+    //   B: P V of tile u (V^T in buffer u%2) while tile u + 1 is masked (DIAG)
+    //      and max-reduced;
+    // rows whose max grew are rescaled after the block.  The mask is applied
+    // only by the DIAG form (tiles that reach the diagonal or the sequence end),
+    // and waves past their last tile only stage (stage_only), so the three
+    // loops below keep every step free of branches.  Barriers match by count:
+    // every wave runs the same (even) number of iterations.  Staging is
+    // unconditional; tiles past the end are zero-filled (or clamped) and land
+    // in buffers nobody reads again.
+    auto step = [&](const int u, Scores &s_cur, Scores &s_nxt, auto diag) {
+      constexpr bool DIAG = decltype(diag)::value;
+      staged();
+      lds_barrier();
+      stage_k(u + 2);
+      stage_v(u + 1);
+      // LLVM's built-in MFMA / LDS-read interleaving strategy for the step's
+      // block (same instructions, another order): 1-2% faster at every shape
+      // measured, with fewer registers.
+      __builtin_amdgcn_iglp_opt(0);
+      const int kt = tb + KSPLIT * u + kh;  // key tile
+      const char *kb = ks_h + ((u + 1) & 1) * TILE;
+      const char *vb = vs_h + (u & 1) * TILE;
+      // ---- A: the NH score chains of tile u + 1 on the matrix cores while
+      // tile u's exp2 / convert / row-sum work runs on the VALU
 #pragma unroll
       for (int hh = 0; hh < NH; ++hh) {
-        const int l2 = lim - (kt + KSPLIT) * BN - 32 * hh;
+        u32x4 kf[8];
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
-          if (8 * (e >> 2) + (e & 3) > l2) s_nxt[hh][e] = -INFINITY;
+        for (int i = 0; i < 8; ++i)
+          kf[i] = *reinterpret_cast<const u32x4 *>(kb + hh * PF_TILE + kfo[i & 1] + 64 * (i >> 1));
+        s_nxt[hh] = mfma32<T>(kf[0], qreg[0], acc0);
+#pragma unroll
+        for (int i = 1; i < 8; ++i) s_nxt[hh] = mfma32<T>(kf[i], qreg[i], s_nxt[hh]);
       }
+      u32x4 pk[NH][2];
+#pragma unroll
+      for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+        for (int e2 = 0; e2 < 8; ++e2) {
+          const float p0 = fast_exp2(s_cur[hh][2 * e2]);
+          const float p1 = fast_exp2(s_cur[hh][2 * e2 + 1]);
+          const uint32_t pp = T::pack_p(p0, p1);
+          l_i = T::dot2(pp, ones, l_i);
+          pk[hh][e2 >> 2][e2 & 3] = pp;
+        }
+      // ---- B: P V of tile u while tile u + 1 is masked and max-reduced
+#pragma unroll
+      for (int hh = 0; hh < NH; ++hh) {
+        u32x4 vf[8];
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+            const char *vp = vb + hh * PF_TILE + vfo[dt];
+            const u32x2 lo = ds_read_tr16(reinterpret_cast<const uint16_t *>(vp + 4 * kk * PF_BLK));
+            const u32x2 hi = ds_read_tr16(reinterpret_cast<const uint16_t *>(vp + (4 * kk + 2) * PF_BLK));
+            vf[dt * 2 + kk] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+          }
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) o[dt] = mfma32<T>(vf[dt * 2 + kk], pk[hh][kk], o[dt]);
+      }
+      if constexpr (!PRESCALED) {
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) s_nxt[hh][e] = __builtin_fmaf(s_nxt[hh][e], c, -m_run);
+      }
+      if constexpr (DIAG) {
+#pragma unroll
+        for (int hh = 0; hh < NH; ++hh) {
+          const int l2 = lim - (kt + KSPLIT) * BN - 32 * hh;
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (8 * (e >> 2) + (e & 3) > l2) s_nxt[hh][e] = -INFINITY;
+        }
+      }
+      const float mx = rowmax(s_nxt);
+      if (__builtin_expect(__ballot(mx > thr) != 0, 0)) rescale(mx, s_nxt);
+    };
+    auto stage_only = [&](const int u) {
+      staged();
+      lds_barrier();
+      stage_k(u + 2);
+      stage_v(u + 1);
+    };
+    // step u needs the mask from u_first on (its next tile KSPLIT (u+1) + kh
+    // reaches n_full); tile KSPLIT u + kh is past this wave's rows from u_end on
+    const int nf_rel = n_full - tb - kh, nw_rel = min(n_wtiles, te) - tb - kh;
+    const int u_first = nf_rel <= KSPLIT ? 0 : (nf_rel + KSPLIT - 1) / KSPLIT - 1;
+    const int u_end = nw_rel <= 0 ? 0 : (nw_rel + KSPLIT - 1) / KSPLIT;
+    const int u1 = u_first & ~1;                      // <= u_end <= n_iter
+    const int u2 = max(u1, min((u_end + 1) & ~1, n_iter));
+    const std::integral_constant<bool, false> plain;
+    const std::integral_constant<bool, true> diag;
+    int u = 0;
+    for (; u < u1; u += 2) {
+      step(u, s_a, s_b, plain);
+      step(u + 1, s_b, s_a, plain);
     }
-    const float mx = rowmax(s_nxt);
-    if (__builtin_expect(__ballot(mx > thr) != 0, 0)) rescale(mx, s_nxt);
-  };
-  auto stage_only = [&](const int u) {
-    staged();
-    lds_barrier();
-    stage_k(u + 2);
-    stage_v(u + 1);
-  };
-  // step u needs the mask from u_first on (its next tile KSPLIT (u+1) + kh
-  // reaches n_full); tile KSPLIT u + kh is past this wave's rows from u_end on
-  const int nf_rel = n_full - tb - kh, nw_rel = min(n_wtiles, te) - tb - kh;
-  const int u_first = nf_rel <= KSPLIT ? 0 : (nf_rel + KSPLIT - 1) / KSPLIT - 1;
-  const int u_end = nw_rel <= 0 ? 0 : (nw_rel + KSPLIT - 1) / KSPLIT;
-  const int u1 = u_first & ~1;                      // <= u_end <= n_iter
-  const int u2 = max(u1, min((u_end + 1) & ~1, n_iter));
-  const std::integral_constant<bool, false> plain;
-  const std::integral_constant<bool, true> diag;
-  int u = 0;
-  for (; u < u1; u += 2) {
-    step(u, s_a, s_b, plain);
-    step(u + 1, s_b, s_a, plain);
-  }
-  for (; u < u2; u += 2) {
-    step(u, s_a, s_b, diag);
-    step(u + 1, s_b, s_a, diag);
-  }
-  for (; u < n_iter; u += 2) {
-    stage_only(u);
-    stage_only(u + 1);
-  }
+    for (; u < u2; u += 2) {
+      step(u, s_a, s_b, diag);
+      step(u + 1, s_b, s_a, diag);
+    }
+    for (; u < n_iter; u += 2) {
+      stage_only(u);
+      stage_only(u + 1);
+    }
 
-  // ---- epilogue: merge the key streams (KSPLIT = 2), normalise, store.
-  // Both streams finish rows: stream kh takes dims OUT_DIMS kh .. +OUT_DIMS-1
-  // of its 32 rows and reads the partner stream's O for those dims, and its
-  // (m, l), from LDS (16-byte lane-major records, conflict-free).  The
-  // finished tile goes through LDS once more so that every store writes whole
-  // rows: OUT_DIMS * 2 bytes of a row by consecutive lanes, 16 bytes each.
-  staged();       // the last staging loads have landed (the epilogue reuses
-  lds_barrier();  // the tile buffers); every wave is done with the K / V^T tiles
-  float *const xo = reinterpret_cast<float *>(lds);  // [kh][rb][8][64 lanes][4]
-  float *const xm = xo + XCH_FLOATS;                 // [kh][rb][2][64 lanes]
-  uint16_t *const ys = reinterpret_cast<uint16_t *>(xm + ML_FLOATS) + w * 32 * YS_PITCH;
-  float s_own, s_oth = 0.f;  // weights of this stream's and the partner's O, 1 / l included
-  const floatx4 *xr = nullptr;
-  if constexpr (KSPLIT == 2) {
-    const float m_own = thr > -INFINITY ? m_run : -INFINITY;
-    floatx4 *const xw = reinterpret_cast<floatx4 *>(xo) + (kh * NRB + rb) * 8 * 64 + lane;
+    // ---- epilogue: merge the key streams (KSPLIT = 2), normalise, store.
+    // Both streams finish rows: stream kh takes dims OUT_DIMS kh .. +OUT_DIMS-1
+    // of its 32 rows and reads the partner stream's O for those dims, and its
+    // (m, l), from LDS (16-byte lane-major records, conflict-free).  The
+    // finished tile goes through LDS once more so that every store writes whole
+    // rows: OUT_DIMS * 2 bytes of a row by consecutive lanes, 16 bytes each.
+    staged();       // the last staging loads have landed (the epilogue reuses
+    lds_barrier();  // the tile buffers); every wave is done with the K / V^T tiles
+    float *const xo = reinterpret_cast<float *>(lds);  // [kh][rb][8][64 lanes][4]
+    float *const xm = xo + XCH_FLOATS;                 // [kh][rb][2][64 lanes]
+    uint16_t *const ys = reinterpret_cast<uint16_t *>(xm + ML_FLOATS) + w * 32 * YS_PITCH;
+    float s_own, s_oth = 0.f;  // weights of this stream's and the partner's O, 1 / l included
+    const floatx4 *xr = nullptr;
+    if constexpr (KSPLIT == 2) {
+      const float m_own = thr > -INFINITY ? m_run : -INFINITY;
+      floatx4 *const xw = reinterpret_cast<floatx4 *>(xo) + (kh * NRB + rb) * 8 * 64 + lane;
 #pragma unroll
-    for (int gq = 0; gq < 8; ++gq) {
-      // the partner's half: o[2 + gq / 4] for stream 0, o[gq / 4] for stream 1
-      // (selects, not an index that depends on kh, keep o in registers)
-      const floatx16 &ox = o[2 + (gq >> 2)], &oy = o[gq >> 2];
-      const int e0 = (gq & 3) * 4;
-      floatx4 x;
+      for (int gq = 0; gq < 8; ++gq) {
+        // the partner's half: o[2 + gq / 4] for stream 0, o[gq / 4] for stream 1
+        // (selects, not an index that depends on kh, keep o in registers)
+        const floatx16 &ox = o[2 + (gq >> 2)], &oy = o[gq >> 2];
+        const int e0 = (gq & 3) * 4;
+        floatx4 x;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = kh == 0 ? ox[e0 + j] : oy[e0 + j];
-      xw[gq * 64] = x;
+        for (int j = 0; j < 4; ++j) x[j] = kh == 0 ? ox[e0 + j] : oy[e0 + j];
+        xw[gq * 64] = x;
+      }
+      xm[((kh * NRB + rb) * 2 + 0) * 64 + lane] = m_own;
+      xm[((kh * NRB + rb) * 2 + 1) * 64 + lane] = l_i;
+      lds_barrier();
+      const int ko = 1 - kh;
+      const float m_oth = xm[((ko * NRB + rb) * 2 + 0) * 64 + lane];
+      const float l_oth = xm[((ko * NRB + rb) * 2 + 1) * 64 + lane];
+      // a state that never saw an unmasked key (m = -inf, l = 0, O = 0) gets
+      // weight 0; stream 0 always sees key 0, so mm is finite on real rows
+      const float mm = fmaxf(m_own, m_oth);
+      // (a part may hold no key of a row in either stream: mm = -inf)
+      const float mmz = SPLITK && mm == -INFINITY ? 0.f : mm;
+      const float a_own = fast_exp2(m_own - mmz), a_oth = fast_exp2(m_oth - mmz);
+      const float l_row = xor32_add(l_i * a_own + l_oth * a_oth);
+      xr = reinterpret_cast<const floatx4 *>(xo) + (ko * NRB + rb) * 8 * 64 + lane;
+      if (SPLITK && n_parts > 1) {
+        // this part's state of the row: O unnormalised (dims OUT_DIMS kh ..),
+        // relative to max mm, and the row sum; straight from the MFMA layout
+        const int grow = r_wave + r32;
+        if (grow < rows_total) {
+          const int p = grow / G, hh = g * G + (grow - p * G);
+          const int64_t pr = (int64_t)part * a.rows_all + ((int64_t)b * S + p) * a.Hq + hh;
+          const int64_t off = pr * PF_HD + OUT_DIMS * kh + 4 * hf;
+          constexpr bool NORM_F16 = T::code == MCE_F16;
+          const float sc = NORM_F16 ? (l_row > 0.f ? 1.0f / l_row : 0.f) : 1.0f;
+#pragma unroll
+          for (int dd = 0; dd < OUT_DIMS / 32; ++dd)
+#pragma unroll
+            for (int e4 = 0; e4 < 4; ++e4) {
+              const floatx4 x = xr[(dd * 4 + e4) * 64];
+              floatx4 v;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const int e = 4 * e4 + j;
+                v[j] = ((kh == 0 ? o[dd][e] : o[2 + dd][e]) * a_own + x[j] * a_oth) * sc;
+              }
+              if constexpr (NORM_F16) {
+                u32x2 h;
+                h[0] = pack2<T>(v[0], v[1]);
+                h[1] = pack2<T>(v[2], v[3]);
+                *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(a.ws_o) + off + 32 * dd +
+                                           8 * e4) = h;
+              } else {
+                *reinterpret_cast<floatx4 *>(a.ws_o + off + 32 * dd + 8 * e4) = v;
+              }
+            }
+          if (kh == 0 && hf == 0)
+            *reinterpret_cast<float2 *>(a.ws_ml + pr * 2) =
+                float2{l_row > 0.f ? mm : -INFINITY, l_row};
+        }
+        return;
+      }
+      const float inv = 1.0f / l_row;
+      s_own = a_own * inv;
+      s_oth = a_oth * inv;
+    } else {
+      s_own = 1.0f / xor32_add(l_i);
     }
-    xm[((kh * NRB + rb) * 2 + 0) * 64 + lane] = m_own;
-    xm[((kh * NRB + rb) * 2 + 1) * 64 + lane] = l_i;
-    lds_barrier();
-    const int ko = 1 - kh;
-    const float m_oth = xm[((ko * NRB + rb) * 2 + 0) * 64 + lane];
-    const float l_oth = xm[((ko * NRB + rb) * 2 + 1) * 64 + lane];
-    // a state that never saw an unmasked key (m = -inf, l = 0, O = 0) gets
-    // weight 0; stream 0 always sees key 0, so mm is finite on real rows
-    const float mm = fmaxf(m_own, m_oth);
-    // (a part may hold no key of a row in either stream: mm = -inf)
-    const float mmz = SPLITK && mm == -INFINITY ? 0.f : mm;
-    const float a_own = fast_exp2(m_own - mmz), a_oth = fast_exp2(m_oth - mmz);
-    const float l_row = xor32_add(l_i * a_own + l_oth * a_oth);
-    xr = reinterpret_cast<const floatx4 *>(xo) + (ko * NRB + rb) * 8 * 64 + lane;
-    if (SPLITK && n_parts > 1) {
-      // this part's state of the row: O unnormalised (dims OUT_DIMS kh ..),
-      // relative to max mm, and the row sum; straight from the MFMA layout
-      const int grow = r_wave + r32;
+    // lane: row r32 of the wave, dims 32 dd + 8 e4 + 4 hf + 0..3 of its half
+#pragma unroll
+    for (int dd = 0; dd < OUT_DIMS / 32; ++dd)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        floatx4 x = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (KSPLIT == 2) x = xr[(dd * 4 + e4) * 64];
+        float v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int e = 4 * e4 + j;
+          const float own = KSPLIT == 2 ? (kh == 0 ? o[dd][e] : o[2 + dd][e]) : o[dd][e];
+          v[j] = own * s_own + x[j] * s_oth;
+        }
+        u32x2 pr;
+        pr[0] = pack2<T>(v[0], v[1]);
+        pr[1] = pack2<T>(v[2], v[3]);
+        *reinterpret_cast<u32x2 *>(&ys[r32 * YS_PITCH + dd * 32 + 8 * e4 + 4 * hf]) = pr;
+      }
+    // the wave reads back rows written by its other lanes: LDS operations of a
+    // wave complete in order, so only the compiler has to keep the order
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    constexpr int CH = OUT_DIMS / 8;  // 16-byte chunks per row
+    constexpr int RPI = 64 / CH;      // rows per store instruction
+    const int dim0 = KSPLIT == 2 ? OUT_DIMS * kh : 0;
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int rr = i * RPI + lane / CH, ch = lane % CH;
+      const u32x4 val = *reinterpret_cast<const u32x4 *>(&ys[rr * YS_PITCH + 8 * ch]);
+      const int grow = r_wave + rr;
       if (grow < rows_total) {
         const int p = grow / G, hh = g * G + (grow - p * G);
-        const int64_t pr = (int64_t)part * a.rows_all + ((int64_t)b * S + p) * a.Hq + hh;
-        const int64_t off = pr * PF_HD + OUT_DIMS * kh + 4 * hf;
-        constexpr bool NORM_F16 = T::code == MCE_F16;
-        const float sc = NORM_F16 ? (l_row > 0.f ? 1.0f / l_row : 0.f) : 1.0f;
-#pragma unroll
-        for (int dd = 0; dd < OUT_DIMS / 32; ++dd)
-#pragma unroll
-          for (int e4 = 0; e4 < 4; ++e4) {
-            const floatx4 x = xr[(dd * 4 + e4) * 64];
-            floatx4 v;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int e = 4 * e4 + j;
-              v[j] = ((kh == 0 ? o[dd][e] : o[2 + dd][e]) * a_own + x[j] * a_oth) * sc;
-            }
-            if constexpr (NORM_F16) {
-              u32x2 h;
-              h[0] = pack2<T>(v[0], v[1]);
-              h[1] = pack2<T>(v[2], v[3]);
-              *reinterpret_cast<u32x2 *>(reinterpret_cast<uint16_t *>(a.ws_o) + off + 32 * dd +
-                                         8 * e4) = h;
-            } else {
-              *reinterpret_cast<floatx4 *>(a.ws_o + off + 32 * dd + 8 * e4) = v;
-            }
-          }
-        if (kh == 0 && hf == 0)
-          *reinterpret_cast<float2 *>(a.ws_ml + pr * 2) =
-              float2{l_row > 0.f ? mm : -INFINITY, l_row};
+        *reinterpret_cast<u32x4 *>(a.out + ((int64_t)b * S + p) * q_row_stride +
+                                   (int64_t)hh * PF_HD + dim0 + 8 * ch) = val;
       }
-      return;
     }
-    const float inv = 1.0f / l_row;
-    s_own = a_own * inv;
-    s_oth = a_oth * inv;
-  } else {
-    s_own = 1.0f / xor32_add(l_i);
-  }
-  // lane: row r32 of the wave, dims 32 dd + 8 e4 + 4 hf + 0..3 of its half
-#pragma unroll
-  for (int dd = 0; dd < OUT_DIMS / 32; ++dd)
-#pragma unroll
-    for (int e4 = 0; e4 < 4; ++e4) {
-      floatx4 x = {0.f, 0.f, 0.f, 0.f};
-      if constexpr (KSPLIT == 2) x = xr[(dd * 4 + e4) * 64];
-      float v[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int e = 4 * e4 + j;
-        const float own = KSPLIT == 2 ? (kh == 0 ? o[dd][e] : o[2 + dd][e]) : o[dd][e];
-        v[j] = own * s_own + x[j] * s_oth;
-      }
-      u32x2 pr;
-      pr[0] = pack2<T>(v[0], v[1]);
-      pr[1] = pack2<T>(v[2], v[3]);
-      *reinterpret_cast<u32x2 *>(&ys[r32 * YS_PITCH + dd * 32 + 8 * e4 + 4 * hf]) = pr;
-    }
-  // the wave reads back rows written by its other lanes: LDS operations of a
-  // wave complete in order, so only the compiler has to keep the order
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
-  constexpr int CH = OUT_DIMS / 8;  // 16-byte chunks per row
-  constexpr int RPI = 64 / CH;      // rows per store instruction
-  const int dim0 = KSPLIT == 2 ? OUT_DIMS * kh : 0;
-#pragma unroll
-  for (int i = 0; i < 32 / RPI; ++i) {
-    const int rr = i * RPI + lane / CH, ch = lane % CH;
-    const u32x4 val = *reinterpret_cast<const u32x4 *>(&ys[rr * YS_PITCH + 8 * ch]);
-    const int grow = r_wave + rr;
-    if (grow < rows_total) {
-      const int p = grow / G, hh = g * G + (grow - p * G);
-      *reinterpret_cast<u32x4 *>(a.out + ((int64_t)b * S + p) * q_row_stride +
-                                 (int64_t)hh * PF_HD + dim0 + 8 * ch) = val;
-    }
-  }
+  }  // items of this workgroup
 }
 
 // Merge of the key parts (SPLITK): 32 threads per query row (4 dims each), 8
@@ -858,10 +909,21 @@ int prefill_paged_parts(int batch, int seq_len, int num_heads, int num_kv_heads)
 template <bool PAGED>
 int prefill_launch(int dtype, PrefillArgs &a, void *stream, const char *name) {
   a.n_items = (int)prefill_items(a.S, a.G);
-  const int64_t grid = (int64_t)a.n_items * a.B * a.Hkv * (a.nsplit > 1 ? a.nsplit : 1);
-  MCE_REQUIRE(grid < ((int64_t)1 << 31), "%s: problem too large", name);
+  const int64_t items = (int64_t)a.n_items * a.B * a.Hkv;
+  MCE_REQUIRE(items * (a.nsplit > 1 ? a.nsplit : 1) < ((int64_t)1 << 31), "%s: problem too large",
+              name);
   hipStream_t st = (hipStream_t)stream;
-  const bool two_streams = grid < 2 * (int64_t)cu_count();
+  const bool two_streams = items < 2 * (int64_t)cu_count();
+  // workgroups per (sequence, kv head): one per item, or, on the two-stream
+  // path when the items outnumber the CUs, one round of at most one per CU,
+  // workgroup j taking item ranks j and 2 per - 1 - j (the kernel derives
+  // per from the grid)
+  int64_t per = a.n_items;
+  if (two_streams && a.nsplit <= 1) {
+    const int64_t c_per = std::max<int64_t>(1, cu_count() / ((int64_t)a.B * a.Hkv));
+    if (a.n_items > c_per) per = std::max<int64_t>(c_per, (a.n_items + 1) / 2);
+  }
+  const int64_t grid = per * a.B * a.Hkv * (a.nsplit > 1 ? a.nsplit : 1);
   if constexpr (PAGED) {
     if (a.nsplit > 1) {
       const unsigned mgrid = (unsigned)((a.rows_all + 7) / 8);
@@ -916,6 +978,9 @@ extern "C" int mce_prefill_attention(int dtype, const void *query,
               "mce_prefill_attention: tensors must be 16-byte aligned");
   const int G = num_heads / num_kv_heads;
   MCE_REQUIRE((int64_t)seq_len * G < ((int64_t)1 << 30), "mce_prefill_attention: sequence too long");
+  // one sequence's queries are addressed with 32-bit byte offsets
+  MCE_REQUIRE((int64_t)seq_len * num_heads * head_dim * 2 < ((int64_t)1 << 31),
+              "mce_prefill_attention: seq_len * num_heads too large");
   // K/V tiles are addressed with 32-bit byte offsets within one batch entry
   // (including the prefetch of up to 6 64-key tiles past the end)
   MCE_REQUIRE(((int64_t)seq_len + 512) * num_kv_heads * head_dim * 2 < ((int64_t)1 << 31),
@@ -975,6 +1040,8 @@ extern "C" int mce_prefill_attention_paged(int dtype, const void *query, const v
   MCE_REQUIRE(num_blocks >= 1, "%s: empty page pool", name);
   const int G = num_heads / num_kv_heads;
   MCE_REQUIRE((int64_t)seq_len * G < ((int64_t)1 << 30), "%s: too many query rows", name);
+  MCE_REQUIRE((int64_t)seq_len * num_heads * head_dim * 2 < ((int64_t)1 << 31),
+              "%s: seq_len * num_heads too large", name);
   const int64_t cache_bytes = num_blocks * block_size * num_kv_heads * head_dim * 2;
   MCE_REQUIRE(cache_bytes < ((int64_t)1 << 31),
               "%s: the page pool must be smaller than 2 GiB (32-bit offsets)", name);

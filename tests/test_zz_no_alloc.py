@@ -51,3 +51,39 @@ def test_noalloc_decode_equals_workspace_decode_twice(dev):
                                big.context_lens, big.scale)
     got = _call("mce_paged_attention_decode_noalloc", big, dev)
     assert (got.float() - ref).abs().max().item() <= 1e-2
+
+
+def test_noalloc_decode_graph_replays(dev):
+    """The use the header names: code under HIP graph capture.  After a first,
+    uncaptured call (which looks up the scratch address), the entry point is
+    recorded in a torch.cuda graph and replayed three times; before each
+    replay an eager call of another shape overwrites the shared scratch, and
+    every replay equals the eager result bit for bit."""
+    case = cfg2_decode()
+    other = make_decode_case(46, 6, cfg2_context_lens(46, 6, 1500, 4000), max_blocks=256)
+    want = _call("mce_paged_attention_decode_noalloc", case, dev)
+    q = case.query.to(dev)
+    kc, vc = case.key_cache.to(dev), case.value_cache.to(dev)
+    bt, cl = case.block_tables.to(dev), case.context_lens.to(dev)
+    b, hq, d = q.shape
+    nb, bs, hkv, _ = kc.shape
+    out = torch.full_like(q, float("nan"))
+    args = [_lib.MCE_F16, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(),
+            cl.data_ptr(), out.data_ptr(), b, hq, hkv, d, case.max_blocks, bs, nb, case.scale]
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):  # warm-up on the capture stream, outside capture
+        _lib.call("mce_paged_attention_decode_noalloc", *args,
+                  torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _lib.call("mce_paged_attention_decode_noalloc", *args,
+                  torch.cuda.current_stream(dev).cuda_stream)
+    for _ in range(3):
+        _call("mce_paged_attention_decode_noalloc", other, dev)  # clobbers the scratch
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize(dev)
+        assert torch.equal(out.cpu().view(torch.int16), want.view(torch.int16))
