@@ -248,11 +248,11 @@ def test_chunked_prefill_matches_one_shot_and_oracle(dev):
 
 
 def test_chunked_prefill_behind_long_prefix_splits_keys(dev):
-    """A 1300-token prompt in 512-position chunks: the third chunk runs behind
-    a 1024-token cached prefix, where prefill_step asks for the key split
-    (one sequence: a 96-workgroup grid, so its query blocks' keys are cut in
-    two parts and merged); logits within the oracle bars."""
-    b, s = 1, 1300
+    """A 2300-token prompt in 512-position chunks: the fifth chunk (252
+    positions) runs behind a 2048-token cached prefix, where prefill_step asks
+    for the key split (one sequence: a small grid, so its query blocks' keys
+    are cut in parts and merged); logits within the oracle bars."""
+    b, s = 1, 2300
     model, cache, ref = build(dev, b, s, 2, tied=False)
     ids = torch.randint(0, CFG["vocab_size"], (b, s), generator=torch.Generator().manual_seed(8))
     chunked = prefill_step(model, ids.to(dev), [0], chunk_size=512)
