@@ -10,7 +10,9 @@
 // Work items: a workgroup takes BM = 32 * NRB consecutive rows of one (b, g).
 // Causal cost grows with the row index, so workgroups are numbered heaviest
 // item first.  Small grids run two key streams per item (even / odd key
-// tiles, 8 waves) merged through LDS at the end.
+// tiles) merged through LDS at the end: 128-row items on 8-wave workgroups,
+// or, when those would leave CUs idle, 64-row items on 4-wave workgroups, two
+// per CU.
 //
 // Each wave owns 32 rows and uses v_mfma_f32_32x32x16_f16 throughout:
 //   S^T[32 keys x 32 rows] = K . Q^T   (A = K from LDS, B = Q^T in registers)
@@ -23,15 +25,16 @@
 // S^T output layout) is mirrored by the V^T operand reads: V is staged
 // row-major like K and read with the transposing ds_read_b64_tr_b16, two per
 // fragment (keys 4(l/32) + 0..3 and 8 + 4(l/32) + 0..3 of a 16-key group), so
-// no transpose runs on the VALU.  K rows are padded by 16 bytes (272-byte
-// pitch: conflict-free 16-byte fragment reads), V rows by 64 bytes (320-byte
-// pitch: each transposing read touches 8 rows x 64 bytes, two per bank).
+// no transpose runs on the VALU.  Tiles sit in LDS in 4-row blocks with
+// permuted 16-byte chunks (layout below), filled by direct-to-LDS buffer
+// loads.
 //
 // Software pipeline: the scores of key tile k+1 are computed in the same
 // straight-line block as the softmax and P V of tile k, so the exp/convert
 // VALU work of one tile runs while the matrix cores work on the other.  K and
 // V^T are double-buffered in LDS (K one tile ahead of V) with one barrier per
-// tile; each tile is fetched into registers one step before it is staged.
+// tile; the loads of a tile are issued one step before the barrier that
+// publishes it.
 //
 // Softmax in the log2 domain: Q is pre-scaled by c = scale log2(e) when it is
 // loaded, and each score accumulator starts at -m (the row's running max, in
@@ -154,7 +157,7 @@ struct PrefillArgs {
 };
 
 constexpr int PF_MAX_BLOCKS = 8192;  // paged mode: block-table row staged in LDS
-constexpr int PF_NRB_MERGE = 4;      // row blocks per item of the launches (PF_NRB)
+constexpr int PF_NRB_MERGE = 4;      // row blocks per item of the paged launches (PF_NRB)
 constexpr int PF_MAX_SPLIT = 8;      // key parts per item (SPLITK)
 // SPLITK: at least this many key tiles per part (a part's start-up, epilogue
 // and partial-state traffic cost about as much as streaming 8 to 16 tiles)
@@ -216,12 +219,11 @@ void prefill_causal_kernel(PrefillArgs a) {
   constexpr int XCH_FLOATS = KSPLIT == 2 ? 2 * NRB * 32 * 64 : 0;
   constexpr int ML_FLOATS = KSPLIT == 2 ? 2 * NRB * 2 * 64 : 0;
   constexpr int EPI_HALFS = 2 * (XCH_FLOATS + ML_FLOATS) + NRB * KSPLIT * 32 * YS_PITCH;
-  // [key stream][double buffer] K tiles, then V tiles, then (two key streams)
-  // the item's Q rows (NRB 32-row groups in the K tile layout); the epilogue
-  // reuses them all.  One-stream launches load Q straight into registers:
-  // their LDS has to leave room for two workgroups per CU, which overlap one
-  // workgroup's start with the other's steps.
-  constexpr bool Q_LDS = KSPLIT == 2;
+  // [key stream][double buffer] K tiles, then V tiles, then (two key streams,
+  // 8 waves) the item's Q rows (NRB 32-row groups in the K tile layout); the
+  // epilogue reuses them all.  The other launches load Q straight into
+  // registers: their LDS has to leave room for two workgroups per CU.
+  constexpr bool Q_LDS = KSPLIT == 2 && NRB == 4;
   constexpr int TILE_HALFS = (2 * KSPLIT * 2 * TILE + (Q_LDS ? NRB * PF_TILE : 0)) / 2;
   constexpr int LDS_HALFS = TILE_HALFS > EPI_HALFS ? TILE_HALFS : EPI_HALFS;
   __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALFS];
@@ -888,8 +890,18 @@ namespace {
 // key range is split over two wave sets when the grid alone would not give
 // every CU about two workgroups (long causal sequences, small batch).
 constexpr int PF_NRB = PF_NRB_MERGE;
+// Contiguous two-stream launches whose 128-row grid would not reach about
+// 1.2 workgroups per CU take 64-row items (PF_NRB_SMALL row blocks) on 4-wave
+// workgroups, two per CU: twice the workgroups over the same rows.  Measured
+// on MI355X (B=1, 24 / 8 heads): S=512 13.0 -> 11.1 us, S=1024 19.1 -> 17.2,
+// S=1536 26.2 -> 24.9; past the threshold (S=1792: 336 128-row items) the
+// halved row block, which stages every K / V tile for half as many rows, is
+// 3-9% slower.
+constexpr int PF_NRB_SMALL = 2;
 
-int64_t prefill_items(int64_t S, int G) { return (S * G + 32 * PF_NRB - 1) / (32 * PF_NRB); }
+int64_t prefill_items(int64_t S, int G, int nrb = PF_NRB) {
+  return (S * G + 32 * nrb - 1) / (32 * nrb);
+}
 
 // Key parts per item of the paged mode: grids that leave more than half of
 // the CUs without a workgroup (few long sequences, a short chunk behind a
@@ -918,9 +930,13 @@ int prefill_launch(int dtype, PrefillArgs &a, void *stream, const char *name) {
   // path when the items outnumber the CUs, one round of at most one per CU,
   // workgroup j taking item ranks j and 2 per - 1 - j (the kernel derives
   // per from the grid)
+  // (small grids, contiguous: 64-row items and two workgroups per CU)
+  const bool small = !PAGED && two_streams && 5 * items <= 6 * (int64_t)cu_count();
+  if (small) a.n_items = (int)prefill_items(a.S, a.G, PF_NRB_SMALL);
   int64_t per = a.n_items;
   if (two_streams && a.nsplit <= 1) {
-    const int64_t c_per = std::max<int64_t>(1, cu_count() / ((int64_t)a.B * a.Hkv));
+    const int64_t c_per =
+        std::max<int64_t>(1, (small ? 2 : 1) * cu_count() / ((int64_t)a.B * a.Hkv));
     if (a.n_items > c_per) per = std::max<int64_t>(c_per, (a.n_items + 1) / 2);
   }
   const int64_t grid = per * a.B * a.Hkv * (a.nsplit > 1 ? a.nsplit : 1);
@@ -940,6 +956,15 @@ int prefill_launch(int dtype, PrefillArgs &a, void *stream, const char *name) {
   // 32-key tiles: 64-key tiles (241 registers) measured 5% slower at cfg3
   // and 8% at B=8 S=512 with the same staging
   constexpr int BN = PF_BN;
+  if constexpr (!PAGED) {
+    if (small) {
+      if (dtype == MCE_F16)
+        prefill_causal_kernel<F16T, PF_NRB_SMALL, 2, false, false, BN><<<(unsigned)grid, PF_NRB_SMALL * 128, 0, st>>>(a);
+      else
+        prefill_causal_kernel<BF16T, PF_NRB_SMALL, 2, false, false, BN><<<(unsigned)grid, PF_NRB_SMALL * 128, 0, st>>>(a);
+      return check_launch(name);
+    }
+  }
   if (dtype == MCE_F16) {
     if (two_streams)
       prefill_causal_kernel<F16T, PF_NRB, 2, PAGED, false, BN><<<(unsigned)grid, PF_NRB * 128, 0, st>>>(a);

@@ -250,6 +250,26 @@ def test_prefill_large_grid_matches_oracle(dev, b, s):
     assert err <= TOL, err
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_prefill_small_and_full_grid_layouts_agree(dev, dtype):
+    """The two two-stream launches compute each row identically: a causal
+    row depends only on the keys up to its position, so the first 1536
+    positions of an S = 1792 call (336 items of 128 rows: 8-wave workgroups)
+    equal, bit for bit, an S = 1536 call on that prefix (288 items: the
+    64-row, 4-wave launch of small grids).  The long call is also checked
+    against the oracle."""
+    case = make_prefill_case(77, 1, 1792, dtype=dtype)
+    q, k, v = (t.to(dev) for t in (case.query, case.key, case.value))
+    full = ops.prefill_attention(q, k, v, case.scale)
+    pre = ops.prefill_attention(q[:, :1536].contiguous(), k[:, :1536].contiguous(),
+                                v[:, :1536].contiguous(), case.scale)
+    torch.cuda.synchronize()
+    assert torch.equal(full[:, :1536].view(torch.int16), pre.view(torch.int16))
+    ref = prefill_attention_ref(case.query, case.key, case.value, case.scale)
+    err = (full.cpu().float() - ref).abs().max().item()
+    assert err <= TOL, err
+
+
 def test_prefill_first_row_is_v0(dev):
     """Row 0 attends to key 0 only, so its output is v_0 up to the rounding of
     p (exactly 1 when the running max is that score) and of the fp16 store."""
