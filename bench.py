@@ -28,6 +28,10 @@ Extra fields on the same JSON line:
             decode steps replayed via hipGraph: tok/s, ms/step, TTFT.
   model_b1  the same at B=1, the shape the reference's engine benchmark
             prints TTFT, inter-token latency and tok/s for.
+  measured_ceilings  context beside the published peaks (which stay the
+            roofline denominators): a 1 GiB device copy's GB/s and a hipBLASLt
+            fp16 8192^3 GEMM's TFLOP/s, with the decode and prefill figures as
+            fractions of them.
   cpu_baseline  the CPU oracle on the same cfg2 inputs, on this host's cores
             (prefill, splitk and model carry their own: cfg3, cfg4, and a
             bounded cfg5 sample -- B=8 prefill of the 512-token prompts then 4
@@ -38,7 +42,7 @@ Extra fields on the same JSON line:
             128 behind 2048, with and without the key split: us, TFLOP/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
-                       [--only decode|prefill|legs|splitk|harness|norms|model|chunked]
+                       [--only decode|prefill|legs|splitk|harness|norms|model|chunked|ceilings]
 (--only runs one workload; only the default run prints the full result line.)
 """
 from __future__ import annotations
@@ -394,6 +398,34 @@ def bench_prefill_vs_sdpa(dev, steps: int) -> list:
     return rows
 
 
+def bench_ceilings(dev, steps: int = 20) -> dict:
+    """Measured ceilings of this GPU, reported beside the published peaks as
+    context (the roofline denominators stay the published 8 TB/s and 2.5
+    PFLOP/s): a 1 GiB device-to-device copy (read + write bytes) and a
+    library fp16 GEMM (torch.matmul -> hipBLASLt, 8192^3, fp32 accumulate)."""
+    out = {}
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    ms = time_gpu(lambda: dst.copy_(src), steps, 10)
+    out["copy"] = {"bytes": 2 * n, "us": round(ms * 1e3, 2),
+                   "gbs": round(2 * n / (ms * 1e-3) / 1e9, 1),
+                   "frac_of_hbm_peak": round(2 * n / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del src, dst
+    m = 8192
+    g = torch.Generator(device=dev).manual_seed(9)
+    a = torch.randn(m, m, generator=g, device=dev).half()
+    b = torch.randn(m, m, generator=g, device=dev).half()
+    ms = time_gpu(lambda: torch.matmul(a, b), steps, 5)
+    tf = 2 * m ** 3 / (ms * 1e-3) / 1e12
+    out["gemm_fp16"] = {"shape": [m, m, m], "us": round(ms * 1e3, 2), "tflops": round(tf, 1),
+                        "frac_of_fp16_dense_peak": round(tf / FP16_DENSE_TFLOPS, 4)}
+    del a, b
+    torch.cuda.empty_cache()
+    log(f"ceilings: copy {out['copy']['gbs']} GB/s, fp16 GEMM {out['gemm_fp16']['tflops']} TFLOP/s")
+    return out
+
+
 def bench_chunked(dev, steps: int, warmup: int) -> dict:
     """Chunked prefill attention from the page pool (ops.prefill_attention_paged):
     synthetic fp16 Q/K/V ~ N(0, 1), 24/8 heads, 16-token pages in a shuffled
@@ -672,7 +704,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["decode", "prefill", "legs", "splitk", "harness", "norms",
-                                       "model", "chunked"],
+                                       "model", "chunked", "ceilings"],
                     default=None)
     ap.add_argument("--calibration-copy", action="store_true",
                     help="first copy 256 MiB device-to-device (a kernel of known traffic, "
@@ -775,6 +807,14 @@ def main() -> None:
 
     if args.only == "chunked":
         extra["chunked"] = bench_chunked(dev, max(20, args.steps // 4), 5)
+
+    if args.only in (None, "ceilings"):
+        extra["measured_ceilings"] = bench_ceilings(dev)
+        c = extra["measured_ceilings"]
+        if "decode" in result:
+            c["decode_frac_of_copy"] = round(result["decode"][2] / c["copy"]["gbs"], 4)
+        if "prefill" in extra:
+            c["prefill_frac_of_gemm"] = round(extra["prefill"]["tflops"] / c["gemm_fp16"]["tflops"], 4)
 
     if "decode" not in result:  # a single non-headline workload was asked for
         print(json.dumps({"metric": METRIC, "only": args.only, **extra}), flush=True)
