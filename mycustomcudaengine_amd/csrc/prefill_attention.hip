@@ -383,8 +383,9 @@ void prefill_causal_kernel(PrefillArgs a) {
 
   const int rows_total = S * G;
   // Items of this workgroup.  Without the key split the launch has P
-  // workgroups per (sequence, kv head), at most one per CU, and workgroup j
-  // takes item ranks j and 2 P - 1 - j (ranks count from the heaviest item):
+  // workgroups per (sequence, kv head), at most one per CU (two for the
+  // 4-wave launch), and workgroup j takes item ranks j and 2 P - 1 - j (ranks
+  // count from the heaviest item):
   // the lightest items run behind medium ones on the same CU instead of as a
   // second round of workgroups, which paid a start-up and a drain each.
   // (two-stream launches only: the one-stream launches have a workgroup per
@@ -429,9 +430,9 @@ void prefill_causal_kernel(PrefillArgs a) {
     //
     // Q, K_0, K_1 and V_0 are fetched together (one memory round trip before
     // the first tile instead of one per dependent stage).  With two key
-    // streams Q comes through LDS like K: whole 256-byte rows per 16-lane
-    // group (the MFMA operand pattern straight from global memory, 32 rows x
-    // 32 bytes per load instruction, keeps the address path busy ~3.5x
+    // streams on 8 waves Q comes through LDS like K: whole 256-byte rows per
+    // 16-lane group (the MFMA operand pattern straight from global memory, 32
+    // rows x 32 bytes per load instruction, keeps the address path busy ~3.5x
     // longer), loaded once for both streams; wave w fills 4-row blocks
     // QB w .. QB w + QB - 1 of the item (rows past the end re-read the last
     // row and are zeroed below).
