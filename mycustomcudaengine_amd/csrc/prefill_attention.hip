@@ -96,9 +96,14 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 // fragment reads (of the other buffer) until the load landed.  The waits the
 // kernel needs are explicit (s_waitcnt vmcnt before the publishing barrier);
 // loads the compiler does not see only make its own vmcnt waits stricter.
+// The asm also carries the wait state that gfx9-family parts need between a
+// scalar write of M0 (which the constraint produces just before it) and an
+// LDS-DMA load: the compiler inserts it before the builtin but cannot insert
+// it into inline asm.  (The scalar offset must come from scalar code or a
+// constant: a v_readfirstlane result would need five more wait states.)
 __device__ __forceinline__ void buffer_load_lds16(i32x4 rsrc, int voff, int soff, unsigned m0) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(voff), "s"(rsrc), "s"(soff),
-               "{m0}"(m0));
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" : : "v"(voff), "s"(rsrc),
+               "s"(soff), "{m0}"(m0));
 }
 
 // Raw buffer descriptor (stride 0, range-checked against `bytes`).
