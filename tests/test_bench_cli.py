@@ -23,5 +23,5 @@ def test_more_than_one_gpu_is_refused():
 def test_help_lists_workloads():
     r = _run("--help")
     assert r.returncode == 0
-    for w in ("decode", "prefill", "splitk", "model", "chunked"):
+    for w in ("decode", "prefill", "splitk", "harness", "norms", "model", "chunked", "ceilings"):
         assert w in r.stdout
