@@ -90,10 +90,11 @@ def _prefill_chunked(model, input_ids: torch.Tensor, seq_ids: List[int],
                           kv[l, 0], kv[l, 1], model.cos_table, model.sin_table,
                           positions.view(-1), slots)
             # keys split over workgroups only behind a long cached prefix
-            # (measured: from 2048 cached tokens the split is 8-50% faster for
-            # chunks of 128-512 tokens; at 1024 the whole-key launch ties or wins)
+            # (measured on MI355X, 24/8 heads: from 1536 cached tokens the split
+            # ties or wins, by 4-21% for chunks of 128-512 tokens at B = 1-4;
+            # at 1024 it is 6% faster to 5% slower, at 512 21% slower)
             attn = prefill_attention_paged(q.view(b, n, hq, d), kv[l, 0], kv[l, 1], tables, ctx,
-                                           model.scale, split_keys=c0 >= 2048)
+                                           model.scale, split_keys=c0 >= 1536)
             x.addmm_(attn.view(b * n, hq * d), model.weights[f"{p}.self_attn.o_proj.weight"].T)
             model._mlp(l, x)
     last = x.view(b, -1, x.size(-1))[:, -1].contiguous()

@@ -248,10 +248,11 @@ def test_chunked_prefill_matches_one_shot_and_oracle(dev):
 
 
 def test_chunked_prefill_behind_long_prefix_splits_keys(dev):
-    """A 2300-token prompt in 512-position chunks: the fifth chunk (252
-    positions) runs behind a 2048-token cached prefix, where prefill_step asks
-    for the key split (one sequence: a small grid, so its query blocks' keys
-    are cut in parts and merged); logits within the oracle bars."""
+    """A 2300-token prompt in 512-position chunks: the fourth and fifth
+    chunks (512 and 252 positions) run behind 1536- and 2048-token cached
+    prefixes, where prefill_step asks for the key split (one sequence: a small
+    grid, so its query blocks' keys are cut in parts and merged); logits
+    within the oracle bars."""
     b, s = 1, 2300
     model, cache, ref = build(dev, b, s, 2, tied=False)
     ids = torch.randint(0, CFG["vocab_size"], (b, s), generator=torch.Generator().manual_seed(8))
