@@ -205,9 +205,12 @@ __global__ __launch_bounds__(256) void kv_store_vec_kernel(
 
 // head_dim 128 with 16-byte aligned rows: one workgroup per KVS_TOK tokens.
 // A pass of the 256 threads covers 16 head rows (16 threads x 16 bytes per
-// 256-byte row); the workgroup's rows are (token, K or V, head) in that order,
-// and every thread issues all of its loads before its stores.  32-bit index
-// math throughout (the host checks the ranges).
+// 256-byte row); the workgroup's rows are (token, K or V, head) in that order.
+// The source rows do not depend on the slots, so every thread issues all of
+// its row and slot loads unconditionally (indices clamped into the batch; a
+// per-lane condition would compile to a branch that waits for each load) and
+// then stores the rows whose slot is valid: one memory round trip per thread.
+// 32-bit index math throughout (the host checks the ranges).
 constexpr int KVS_TOK = 4;
 constexpr int KVS_MAX_PASS = 8;  // rows per thread: 2 * heads * KVS_TOK / 16
 
@@ -218,32 +221,32 @@ __global__ __launch_bounds__(256) void kv_store_d128_kernel(
     int64_t vs_tok, int64_t vs_head) {
   const int p = threadIdx.x & 15, r0 = threadIdx.x >> 4;
   const int rows = 2 * heads * KVS_TOK;
+  const int npass = (rows + 15) >> 4;  // uniform
   const int t0 = blockIdx.x * KVS_TOK;
   u32x4 val[KVS_MAX_PASS];
-  int64_t dst[KVS_MAX_PASS];
+  int32_t sl[KVS_MAX_PASS];
 #pragma unroll
   for (int j = 0; j < KVS_MAX_PASS; ++j) {
-    const int r = r0 + 16 * j;
-    dst[j] = -1;
-    val[j] = u32x4{0, 0, 0, 0};
-    if (r >= rows) continue;
+    if (j >= npass) break;
+    const int r = min(r0 + 16 * j, rows - 1);
     const int tt = r / (2 * heads), rem = r - tt * 2 * heads;
-    const int t = t0 + tt;
-    if (t >= num_tokens) continue;
+    const int t = min(t0 + tt, num_tokens - 1);
     const bool is_v = rem >= heads;
     const int h = is_v ? rem - heads : rem;
-    const int64_t sl = slots[t];
-    if (sl < 0 || sl >= num_slots) continue;
     const uint16_t *src = is_v ? value + t * vs_tok + h * vs_head : key + t * ks_tok + h * ks_head;
     val[j] = *reinterpret_cast<const u32x4 *>(src + 8 * p);
-    dst[j] = ((sl * heads + h) * 128 + 8 * p) | ((int64_t)is_v << 62);
+    sl[j] = slots[t];
   }
 #pragma unroll
   for (int j = 0; j < KVS_MAX_PASS; ++j) {
-    if (dst[j] < 0) continue;
-    const bool is_v = (dst[j] >> 62) & 1;
-    const int64_t off = dst[j] & ~((int64_t)1 << 62);
-    *reinterpret_cast<u32x4 *>((is_v ? vc : kc) + off) = val[j];
+    if (j >= npass) break;
+    const int r = r0 + 16 * j;
+    const int tt = r / (2 * heads), rem = r - tt * 2 * heads;
+    const bool is_v = rem >= heads;
+    const int h = is_v ? rem - heads : rem;
+    const int64_t s = sl[j];
+    if (r < rows && t0 + tt < num_tokens && s >= 0 && s < num_slots)
+      *reinterpret_cast<u32x4 *>((is_v ? vc : kc) + (s * heads + h) * 128 + 8 * p) = val[j];
   }
 }
 
