@@ -15,6 +15,11 @@ import shutil
 import subprocess
 import sys
 
+if __package__:
+    from . import asm_check
+else:  # run as a script
+    import asm_check
+
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 REPO_DIR = os.path.dirname(PKG_DIR)
 CSRC = os.path.join(PKG_DIR, "csrc")
@@ -28,6 +33,8 @@ SOURCES = [
     "decode_gemm.hip",
     "decode_loop.hip",
 ]
+# sources whose inline-asm buffer loads are scanned for missing wait states
+ASM_CHECKED = ["prefill_attention.hip"]
 ARCH = "gfx950"
 
 
@@ -57,8 +64,10 @@ def compile_flags() -> list[str]:
 
 def _run(cmd: list[str]) -> None:
     res = subprocess.run(cmd, capture_output=True, text=True)
-    # hipcc's host pass warns that it does not know the packed-fp32 feature.
-    err = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature,
+    # and a device-only -S compile that --hip-link goes unused.
+    err = "\n".join(l for l in res.stderr.splitlines()
+                    if "packed-fp32-ops" not in l and "'--hip-link'" not in l)
     if res.returncode != 0:
         raise RuntimeError(f"command failed ({res.returncode}): {' '.join(cmd)}\n{err}")
     if err.strip():
@@ -76,12 +85,28 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
         obj = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
         objs.append(obj)
         cmds.append([cc, *flags, "-c", os.path.join(CSRC, src), "-o", obj])
+    # gfx950 assembly of the sources with inline-asm loads, for the wait-state
+    # scan below
+    asm_files = []
+    for src in ASM_CHECKED:
+        out = os.path.join(BUILD_DIR, src.replace(".hip", ".s"))
+        asm_files.append(out)
+        cmds.append([cc, *flags, "--cuda-device-only", "-S", os.path.join(CSRC, src), "-o", out])
     jobs = jobs or min(len(cmds), os.cpu_count() or 1, 8)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         for cmd, fut in zip(cmds, [ex.submit(_run, c) for c in cmds]):
             if verbose:
                 print(" ".join(cmd))
             fut.result()
+    # The compiler inserts no wait states for instructions inside inline asm;
+    # a library whose inline-asm loads could read a stale SGPR is refused
+    # (such a load can fault the GPU).
+    for path in asm_files:
+        with open(path) as f:
+            bad = asm_check.check(f.read())
+        if bad:
+            raise RuntimeError(f"{os.path.basename(path)}: {len(bad)} inline-asm wait-state "
+                               "violation(s):\n  " + "\n  ".join(bad[:20]))
     tmp = LIB_PATH + ".tmp"
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
     os.replace(tmp, LIB_PATH)
