@@ -190,7 +190,9 @@ template <class T>
 __device__ inline u32x4 rope_apply(const u32x4 x, const RopeCS &r, int lr) {
   u32x4 pt;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) pt[k] = (uint32_t)__shfl_xor((int)x[k], 8, 64);
+  // lane lr ^ 8 of the same 16-lane row: DPP row_ror:8 (no LDS round trip)
+  for (int k = 0; k < 4; ++k)
+    pt[k] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x[k], 0x128, 0xf, 0xf, false);
   const bool lo_half = lr < 8;
   u32x4 o;
 #pragma unroll
@@ -474,8 +476,7 @@ void paged_decode_kernel(DecodeArgs a) {
           float mx = sc[0][h];
 #pragma unroll
           for (int s8 = 1; s8 < TPG; ++s8) mx = fmaxf(mx, sc[s8][h]);
-          mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          mx = xor32_max(xor16_max(mx));
           mx = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, mx)));
           const float mn = fmaxf(m_run[h], mx);
           alpha[h] = fast_exp2((m_run[h] - mn) * c);
@@ -593,15 +594,11 @@ void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       float v = l_grp[h];
-      v += __shfl_xor(v, 16, 64);
-      v += __shfl_xor(v, 32, 64);
-      l_tot[h] = v;
+      l_tot[h] = xor32_add(xor16_add(v));
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         float x = acc[h][e];
-        x += __shfl_xor(x, 16, 64);
-        x += __shfl_xor(x, 32, 64);
-        acc[h][e] = x;
+        acc[h][e] = xor32_add(xor16_add(x));
       }
     }
     const int64_t row0 = (int64_t)b * a.Hq + head0;

@@ -138,20 +138,38 @@ __device__ inline float row16_sum(float v) {
   return v;
 }
 
-// Full 64-lane sum; every lane gets the result.
-__device__ inline float wave_sum(float v) {
-  v = row16_sum(v);
-  v += __shfl_xor(v, 16, 64);
-  v += __shfl_xor(v, 32, 64);
-  return v;
+// Exchanges across 16-lane rows on the VALU.  v_permlane16_swap swaps the
+// odd rows of one operand with the even rows of the other, and
+// v_permlane32_swap the two 32-lane halves; given x twice, each leaves every
+// lane holding x[l] and x[l ^ 16] (x[l ^ 32]), in some order.  Max and the
+// sum of two values do not depend on that order, so both lanes of a pair get
+// the same result, bit for bit -- what a __shfl_xor (an LDS-routed
+// ds_bpermute, ~100 cycles of latency) would give.
+__device__ __forceinline__ float xor16_max(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ __forceinline__ float xor16_add(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ __forceinline__ float xor32_add(float x) {
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
 }
 
-__device__ inline float wave_max(float v) {
-  v = row16_max(v);
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
-}
+// Full 64-lane sum; every lane gets the result.
+__device__ inline float wave_sum(float v) { return xor32_add(xor16_add(row16_sum(v))); }
+
+__device__ inline float wave_max(float v) { return xor32_max(xor16_max(row16_max(v))); }
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

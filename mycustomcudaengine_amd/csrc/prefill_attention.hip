@@ -120,21 +120,6 @@ __device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t *p) {
       u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)p));
 }
 
-// max(x[l], x[l ^ 32]) in every lane: v_permlane32_swap exchanges the two
-// 32-lane halves, leaving each lane with both values of its pair.
-__device__ __forceinline__ float xor32_max(float x) {
-  const unsigned u = __builtin_bit_cast(unsigned, x);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
-}
-
-// x[l] + x[l ^ 32] in every lane (the same sum in both lanes of a pair).
-__device__ __forceinline__ float xor32_add(float x) {
-  const unsigned u = __builtin_bit_cast(unsigned, x);
-  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
-}
-
 
 struct PrefillArgs {
   const uint16_t *q, *k, *v;
