@@ -253,12 +253,15 @@ def bench_norms(dev, steps: int, warmup: int, compiled: bool = False) -> dict:
     RMSNorm at the reference harness shape (tests/test_ops.py:17-61:
     [8, 2048, 4096] fp16, eps 1e-5) and at cfg5's prefill rows (8 x 512 tokens x
     3072); SwiGLU at cfg5's prefill gate_up [4096, 16384] -> [4096, 8192].  Each
-    timed with HIP events over back-to-back eager calls (median of 5 windows),
-    beside what the reference compares with on the same GPU: torch's fused
-    F.rms_norm (nn.RMSNorm) and the unfused eager formula, F.silu(g) * u for
-    SwiGLU, and with `compiled` torch.compile of the unfused RMSNorm (a Triton
-    kernel; --only norms).  Algorithmic bytes: the input read once, the output
-    written once, plus the weight row."""
+    timed as 20 calls captured in one hipGraph and replayed (`us`; the Python
+    call of an op takes longer than the few-microsecond kernels, so eager
+    back-to-back calls measure the host; `eager_us` reports them too), beside
+    what the reference compares with on the same GPU, timed the same way:
+    torch's fused F.rms_norm (nn.RMSNorm) and the unfused formula, F.silu(g) * u
+    for SwiGLU, and with `compiled` torch.compile of the unfused RMSNorm (a
+    Triton kernel; --only norms; timed eagerly if its capture fails).
+    Algorithmic bytes: the input read once, the output written once, plus the
+    weight row."""
     import my_cuda_engine_cpp as ops
     g = torch.Generator(device=dev).manual_seed(48)
     out = {}
@@ -274,21 +277,28 @@ def bench_norms(dev, steps: int, warmup: int, compiled: bool = False) -> dict:
         x = torch.randn(*shape, generator=g, device=dev).half()
         w = (1.0 + 0.1 * torch.randn(h, generator=g, device=dev)).half()
         nbytes = 2 * x.numel() * 2 + h * 2
-        ms = time_gpu(lambda: ops.rmsnorm(x, w, 1e-5), steps, warmup)
-        row = {"shape": list(shape), "bytes": nbytes, **rate(nbytes, ms)}
-        nms = time_gpu(lambda: torch.nn.functional.rms_norm(x, (h,), w, 1e-5), steps, warmup)
+        ms = time_graph_batch(lambda: ops.rmsnorm(x, w, 1e-5))
+        row = {"shape": list(shape), "bytes": nbytes, **rate(nbytes, ms),
+               "eager_us": round(time_gpu(lambda: ops.rmsnorm(x, w, 1e-5), steps, warmup) * 1e3, 2)}
+        nms = time_graph_batch(lambda: torch.nn.functional.rms_norm(x, (h,), w, 1e-5))
         row["torch_rms_norm_us"] = round(nms * 1e3, 2)
         row["speedup_vs_torch_rms_norm"] = round(nms / ms, 2)
 
         def unfused(x_):
             return x_ * torch.rsqrt(x_.pow(2).mean(-1, keepdim=True) + 1e-5) * w
-        ums = time_gpu(lambda: unfused(x), steps, warmup)
-        row["unfused_eager_us"] = round(ums * 1e3, 2)
+        ums = time_graph_batch(lambda: unfused(x))
+        row["unfused_us"] = round(ums * 1e3, 2)
         if compiled:
             try:
                 cfn = torch.compile(unfused)
                 cfn(x)
-                cms = time_gpu(lambda: cfn(x), steps, warmup)
+                try:
+                    cms = time_graph_batch(lambda: cfn(x))
+                    row["torch_compile_timing"] = "hipGraph of 20 calls"
+                except Exception:  # capture refused: time it eagerly
+                    torch.cuda.synchronize()
+                    cms = time_gpu(lambda: cfn(x), steps, warmup)
+                    row["torch_compile_timing"] = "eager calls"
                 row["torch_compile_us"] = round(cms * 1e3, 2)
                 row["speedup_vs_torch_compile"] = round(cms / ms, 2)
             except Exception as e:  # no working compiler backend on this box
@@ -299,10 +309,11 @@ def bench_norms(dev, steps: int, warmup: int, compiled: bool = False) -> dict:
     t, inter = 4096, 8192
     gu = torch.randn(t, 2 * inter, generator=g, device=dev).half()
     nbytes = gu.numel() * 2 + t * inter * 2
-    ms = time_gpu(lambda: ops.swiglu(gu), steps, warmup)
-    row = {"shape": [t, 2 * inter], "bytes": nbytes, **rate(nbytes, ms)}
+    ms = time_graph_batch(lambda: ops.swiglu(gu))
+    row = {"shape": [t, 2 * inter], "bytes": nbytes, **rate(nbytes, ms),
+           "eager_us": round(time_gpu(lambda: ops.swiglu(gu), steps, warmup) * 1e3, 2)}
     gate, up = gu[:, :inter], gu[:, inter:]
-    tms = time_gpu(lambda: torch.nn.functional.silu(gate) * up, steps, warmup)
+    tms = time_graph_batch(lambda: torch.nn.functional.silu(gate) * up)
     row["torch_silu_mul_us"] = round(tms * 1e3, 2)
     row["speedup_vs_torch"] = round(tms / ms, 2)
     out["swiglu_cfg5_prefill"] = row

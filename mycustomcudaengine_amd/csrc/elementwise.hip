@@ -10,20 +10,26 @@ namespace mce {
 // =========================================================================
 // RMSNorm  (reference: csrc/kernels/rmsnorm.cu:35-108)
 //
-// One wave per row (4 rows per 256-thread workgroup).  The row stays in
+// One wave per row, a workgroup of its own (one-wave workgroups spread the
+// rows over more CUs than four-row ones: 16384 x 4096 40.1 -> 38.6 us, 4096 x
+// 3072 9.1 -> 6.7 us on MI355X, with the stores below; 20-call graphs).  The row stays in
 // registers between the sum-of-squares pass and the scaling pass, so every
 // input byte is read once: VPT 16-byte vectors per lane cover rows up to
-// 512 * VPT elements.  Rows longer than that (or not 16-byte aligned) take
-// the two-pass kernel, whose second read hits L2.
+// 512 * VPT elements.  The output goes out with non-temporal stores (it is
+// not read again by this kernel; plain stores measured 2-28% slower).  Rows
+// longer than 8192 elements (or not 16-byte aligned) take the two-pass
+// kernel, whose second read hits L2.
 // =========================================================================
 template <class T, int VPT>
-__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(
+__global__ __launch_bounds__(64) void rmsnorm_vec_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ w,
     uint16_t *__restrict__ y, int64_t rows, int hidden, int64_t in_stride,
     int64_t out_stride, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  // one row per workgroup (a loop over rows let the compiler wait for the
+  // first of a row's loads before issuing the rest: 38.6 -> 40.4 us at
+  // 16384 x 4096)
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
   const int nvec = hidden >> 3;  // 8 elements per 16-byte vector
   const u32x4 *xr = reinterpret_cast<const u32x4 *>(x + row * in_stride);
   const u32x4 *wr = reinterpret_cast<const u32x4 *>(w);
@@ -33,27 +39,42 @@ __global__ __launch_bounds__(256) void rmsnorm_vec_kernel(
   // exec-masked branch that waits for the loads before it, which kept one
   // 16-byte load per wave in flight and halved the bandwidth.  A zeroed chunk
   // adds fma(0, 0, ss) = ss, so the sum is the one over the row's chunks.
-  // The weight loads go out with the row loads, ahead of the reduction.
+  // The weight loads go out right behind the row loads, ahead of the
+  // reduction: the scheduling barrier keeps the scheduler from sinking them
+  // past it (one more round trip per row).
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int idx = lane + i * 64;
+    v[i] = xr[idx < nvec ? idx : nvec - 1];
+  }
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int idx = lane + i * 64;
     wv[i] = wr[idx < nvec ? idx : nvec - 1];
   }
+  __builtin_amdgcn_sched_barrier(0);
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
     const int idx = lane + i * 64;
-    const u32x4 t = xr[idx < nvec ? idx : nvec - 1];
-    v[i] = idx < nvec ? t : u32x4{0, 0, 0, 0};
+    v[i] = idx < nvec ? v[i] : u32x4{0, 0, 0, 0};
     ss = sumsq8<T>(v[i], ss);
   }
   ss = wave_sum(ss);
   const float inv = rms_inv(ss, hidden, eps);
+  // outputs computed unconditionally, then stored where in the row (the
+  // empty asm takes each one in registers, so that neither the computation
+  // nor its weight load sinks into the store's branch: one more round trip)
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    v[i] = rms_scale8<T>(v[i], wv[i], inv);
+    asm volatile("" : "+v"(v[i]));
+  }
   u32x4 *yr = reinterpret_cast<u32x4 *>(y + row * out_stride);
 #pragma unroll
   for (int i = 0; i < VPT; ++i) {
-    int idx = lane + i * 64;
-    if (idx < nvec) yr[idx] = rms_scale8<T>(v[i], wv[i], inv);
+    const int idx = lane + i * 64;
+    if (idx < nvec) __builtin_nontemporal_store(v[i], yr + idx);
   }
 }
 
@@ -85,26 +106,29 @@ static int rmsnorm_launch(const void *input, const void *weight, void *output,
   const uint16_t *x = (const uint16_t *)input;
   const uint16_t *w = (const uint16_t *)weight;
   uint16_t *y = (uint16_t *)output;
-  dim3 grid((unsigned)((rows + 3) / 4)), block(256);
   const bool vec = hidden % 8 == 0 && in_stride % 8 == 0 &&
                    out_stride % 8 == 0 && aligned16(x) && aligned16(w) &&
                    aligned16(y);
   const int nvec = (int)(hidden / 8);
   int h = (int)hidden;
+  // vector kernels: one 64-lane workgroup per row (the entry point keeps
+  // rows below 2^31)
+  const dim3 vgrid((unsigned)rows), vblock(64);
   if (vec && nvec <= 64)
-    rmsnorm_vec_kernel<T, 1><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+    rmsnorm_vec_kernel<T, 1><<<vgrid, vblock, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
   else if (vec && nvec <= 128)
-    rmsnorm_vec_kernel<T, 2><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+    rmsnorm_vec_kernel<T, 2><<<vgrid, vblock, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
   else if (vec && nvec <= 256)
-    rmsnorm_vec_kernel<T, 4><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+    rmsnorm_vec_kernel<T, 4><<<vgrid, vblock, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
   else if (vec && nvec <= 384)
-    rmsnorm_vec_kernel<T, 6><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+    rmsnorm_vec_kernel<T, 6><<<vgrid, vblock, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
   else if (vec && nvec <= 512)
-    rmsnorm_vec_kernel<T, 8><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+    rmsnorm_vec_kernel<T, 8><<<vgrid, vblock, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
   else if (vec && nvec <= 1024)
-    rmsnorm_vec_kernel<T, 16><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+    rmsnorm_vec_kernel<T, 16><<<vgrid, vblock, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
   else
-    rmsnorm_generic_kernel<T><<<grid, block, 0, st>>>(x, w, y, rows, h, in_stride, out_stride, eps);
+    rmsnorm_generic_kernel<T><<<dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, st>>>(
+        x, w, y, rows, h, in_stride, out_stride, eps);
   return check_launch("mce_rmsnorm");
 }
 
@@ -572,7 +596,7 @@ extern "C" int mce_rmsnorm(int dtype, const void *input, const void *weight,
               "mce_rmsnorm: row stride smaller than hidden size");
   if (rows == 0) return MCE_OK;
   MCE_REQUIRE(input && weight && output, "mce_rmsnorm: null pointer");
-  MCE_REQUIRE((rows + 3) / 4 < (int64_t)1 << 31, "mce_rmsnorm: too many rows");
+  MCE_REQUIRE(rows < ((int64_t)1 << 31) - 1, "mce_rmsnorm: too many rows");
   hipStream_t st = (hipStream_t)stream;
   return dtype == MCE_F16
              ? rmsnorm_launch<F16T>(input, weight, output, rows, hidden, in_row_stride, out_row_stride, eps, st)
