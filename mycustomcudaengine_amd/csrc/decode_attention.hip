@@ -127,12 +127,7 @@ __device__ int build_tile_prefix(const DecodeArgs &a, int *pre, int *wave_tot, i
     if (b < a.B) ctx_out[b] = cb;
     int v = (cb + TILE - 1) / TILE;
     if (v > 0) v += SEG_TILES;
-    int incl = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-      const int o = __shfl_up(incl, d, 64);
-      if (lane >= d) incl += o;
-    }
+    const int incl = wave_incl_scan(v);
     if (lane == 63) wave_tot[w] = incl;
     lds_barrier();
     int before = carry;

@@ -166,6 +166,26 @@ __device__ __forceinline__ float xor32_add(float x) {
   return __builtin_bit_cast(float, (unsigned)r[0]) + __builtin_bit_cast(float, (unsigned)r[1]);
 }
 
+// Inclusive prefix sum over the 64 lanes, all in DPP (gfx9-family): a
+// log-step scan inside each 16-lane row (row_shr 1, 2, 4, 8, lanes shifted in
+// from outside the row read 0), then lane 15 of rows 0 and 2 added to rows 1
+// and 3 (row_bcast:15) and lane 31 to rows 2 and 3 (row_bcast:31).  Integer
+// adds, so the result is exact; no LDS round trips (a __shfl_up is a
+// ds_bpermute).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, true);
+}
+__device__ inline int wave_incl_scan(int v) {
+  v += dpp_i<0x111, 0xf>(v);  // row_shr:1
+  v += dpp_i<0x112, 0xf>(v);  // row_shr:2
+  v += dpp_i<0x114, 0xf>(v);  // row_shr:4
+  v += dpp_i<0x118, 0xf>(v);  // row_shr:8
+  v += dpp_i<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_i<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return v;
+}
+
 // Full 64-lane sum; every lane gets the result.
 __device__ inline float wave_sum(float v) { return xor32_add(xor16_add(row16_sum(v))); }
 
