@@ -566,9 +566,9 @@ void prefill_causal_kernel(PrefillArgs a) {
 
     // Iteration u (key tile kt = KSPLIT u + kh), one straight-line block after
     // the barrier that publishes K_{u+1} and V_u:
-    //   K_{u+2} / V_{u+1} are staged (direct-to-LDS loads) into the buffers
-    //      that iteration u - 1 finished reading; they have the whole
-    //      iteration to land;
+    //   K_{u+2} / V_{u+1} are staged (direct-to-LDS loads, issued after the
+    //      first score MFMA) into the buffers that iteration u - 1 finished
+    //      reading; they have the rest of the iteration to land;
     //   A: scores of tile u + 1 (K in buffer (u+1)%2, accumulators starting at
     //      -m_run) on the matrix cores while the exp2 / convert / row-sum work
     //      of tile u runs on the VALU;
@@ -585,8 +585,6 @@ void prefill_causal_kernel(PrefillArgs a) {
       constexpr bool DIAG = decltype(diag)::value;
       staged();
       lds_barrier();
-      stage_k(u + 2);
-      stage_v(u + 1);
       // LLVM's built-in MFMA / LDS-read interleaving strategy for the step's
       // block (same instructions, another order): 1-2% faster at every shape
       // measured, with fewer registers.
@@ -603,6 +601,14 @@ void prefill_causal_kernel(PrefillArgs a) {
         for (int i = 0; i < 8; ++i)
           kf[i] = *reinterpret_cast<const u32x4 *>(kb + hh * PF_TILE + kfo[i & 1] + 64 * (i >> 1));
         s_nxt[hh] = mfma32<T>(kf[0], qreg[0], acc0);
+        // The staging loads leave once the first score MFMA is issued: the
+        // fragment reads that feed the matrix cores go first after the
+        // barrier (issued before them, the loads and their M0 writes delayed
+        // the step's first MFMA; ~2.5 % of cfg3).
+        if (hh == 0) {
+          stage_k(u + 2);
+          stage_v(u + 1);
+        }
 #pragma unroll
         for (int i = 1; i < 8; ++i) s_nxt[hh] = mfma32<T>(kf[i], qreg[i], s_nxt[hh]);
       }
