@@ -247,6 +247,8 @@ void paged_decode_kernel(DecodeArgs a) {
   u32x4 kx_new{}, vx_new{}, q_pre[G];
   __shared__ u32x4 knv_lds[32];  // rotated k (lanes 0-15) and v (16-31) of the new token
   u32x4 kA[TPG], vA[TPG];  // the wave's first tile (fused mode: fetched in the prologue)
+  int64_t phys_f = 0;      // fused mode: physical block and first row of those rows
+  int tv_f = 0;
   if (a.per_seq) {
     seg0 = 0;
     // one workgroup per (head group, sequence j): a one-sequence tile space
@@ -290,6 +292,8 @@ void paged_decode_kernel(DecodeArgs a) {
     }
     if constexpr (FUSED) {
       const int64_t phys = idf < 0 ? 0 : (idf > nb_hi ? nb_hi : idf);
+      phys_f = phys;
+      tv_f = tvf;
       const int64_t ss = (int64_t)a.Hkv * HD;
       const int64_t off = ((phys << bs_log2) + (tvf & (bs - 1))) * ss + (int64_t)g * HD + lr * 8;
 #pragma unroll
@@ -417,10 +421,21 @@ void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
         for (int s8 = 0; s8 < TPG; ++s8) vv[s8] = ld_nt(vbase + off + s8 * slot_stride);
       };
-      auto load_tile = [&](int t0, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG]) {
+      // Fused append: the row (0 .. TPG - 1) of the lane group's rows tv ..
+      // tv + TPG - 1 of physical block phys that is the new token's slot, or
+      // -1 (the rows lie in one block: bs >= TPG and TPG | tv).  Found when
+      // the tile is loaded, so the tile's compute only tests it.
+      auto patch_row = [&](int64_t phys, int tv) {
+        if (!FUSED || slot_j < 0 || phys != (slot_j >> bs_log2)) return -1;
+        const int dd = (int)(slot_j & (bs - 1)) - (tv & (bs - 1));
+        return dd >= 0 && dd < TPG ? dd : -1;
+      };
+      auto load_tile = [&](int t0, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG], int &sub) {
         int tv = t0 + TPG * lg;
         tv = tv < t_end ? tv : t0;
-        load_rows(blk_lds[(tv >> bs_log2) - first_blk], tv, kk, vv);
+        const int phys = blk_lds[(tv >> bs_log2) - first_blk];
+        load_rows(phys, tv, kk, vv);
+        sub = patch_row(phys, tv);
       };
       int k = rlane;
       if (!a.per_seq) {
@@ -447,6 +462,9 @@ void paged_decode_kernel(DecodeArgs a) {
       // ---- compute of one tile ----
       auto tile_body = [&](int t0, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG]) {
         const int tv = t0 + TPG * lg;
+        // the tile reaches the end of the range (wave-uniform): only such a
+        // tile masks tokens
+        const bool tail = t0 + TILE > t_end;
         // scores: 4 v_dot2 over the lane's 8 dims, then a 16-lane DPP sum;
         // every lane of a group ends with the scores of the group's 8 tokens
         float sc[TPG][G];
@@ -460,9 +478,14 @@ void paged_decode_kernel(DecodeArgs a) {
               // (explicit conversions: bit_cast of an ext-vector element picks
               // element 0 in this compiler)
               d = T::dot2((uint32_t)kk[s8][k], (uint32_t)qv[h][k], d);
-            d = row16_sum(d);
-            sc[s8][h] = tv + s8 < t_end ? d : -INFINITY;
+            sc[s8][h] = row16_sum(d);
           }
+        if (tail) {
+#pragma unroll
+          for (int s8 = 0; s8 < TPG; ++s8)
+#pragma unroll
+            for (int h = 0; h < G; ++h) sc[s8][h] = tv + s8 < t_end ? sc[s8][h] : -INFINITY;
+        }
         // online softmax in base 2: p = exp2(s c - m c)
         float alpha[G];
         bool rescale = false;
@@ -503,9 +526,11 @@ void paged_decode_kernel(DecodeArgs a) {
             for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
         }
         // tokens past the end: zero their V rows (p is 0, V may be NaN garbage)
+        if (tail) {
 #pragma unroll
-        for (int s8 = 0; s8 < TPG; ++s8)
-          if (tv + s8 >= t_end) vv[s8] = u32x4{0, 0, 0, 0};
+          for (int s8 = 0; s8 < TPG; ++s8)
+            if (tv + s8 >= t_end) vv[s8] = u32x4{0, 0, 0, 0};
+        }
         // acc += P V over token pairs with v_dot2
 #pragma unroll
         for (int sp = 0; sp < TPG / 2; ++sp) {
@@ -521,23 +546,14 @@ void paged_decode_kernel(DecodeArgs a) {
           }
         }
       };
-      // Fused append: rows the tile read from the new token's slot are
-      // replaced by the LDS copy (load_tile read tokens tvc .. tvc + 7 of one
-      // block per lane group).  Wave-uniform branch: only the tile holding
+      // Fused append: the row the tile read from the new token's slot (sub,
+      // found when the tile was loaded) is replaced by the LDS copy.
+      // Wave-uniform branch: only the tile holding
       // the slot is patched, in place, every row by a select (a conditional
       // write of one row would become an indexed register write, which puts
       // the tile in scratch memory).
-      auto compute_tile = [&](int t0, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG]) {
-        int sub = -1;
-        if (FUSED && slot_j >= 0) {
-          const int tv = t0 + TPG * lg;
-          const int tvc = tv < t_end ? tv : t0;
-          const int64_t slot0 =
-              ((int64_t)blk_lds[(tvc >> bs_log2) - first_blk] << bs_log2) + (tvc & (bs - 1));
-          const int64_t dd = slot_j - slot0;
-          sub = dd >= 0 && dd < TPG ? (int)dd : -1;
-        }
-        if (__builtin_expect(__ballot(sub >= 0) != 0, 0)) {
+      auto compute_tile = [&](int t0, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG], const int sub) {
+        if (FUSED && __builtin_expect(__ballot(sub >= 0) != 0, 0)) {
           const u32x4 kn = knv_lds[lr], vn = knv_lds[16 + lr];
 #pragma unroll
           for (int s8 = 0; s8 < TPG; ++s8) {
@@ -553,7 +569,8 @@ void paged_decode_kernel(DecodeArgs a) {
       };
 
       // ---- tile loop: compute the tile in registers, then fetch the wave's next ----
-      if (!FUSED && a.per_seq && k < ntile) load_tile(s_lo + TILE * k, kA, vA);
+      int subA = -1;  // patch row of the tile in kA / vA
+      if (!FUSED && a.per_seq && k < ntile) load_tile(s_lo + TILE * k, kA, vA, subA);
       if constexpr (FUSED) {
         // (per-sequence mode: every wave of the workgroup is active and
         // reaches this barrier)  RoPE of the query rows and, by wave 0, of the
@@ -577,10 +594,11 @@ void paged_decode_kernel(DecodeArgs a) {
         }
         lds_barrier();
       }
+      if constexpr (FUSED) subA = patch_row(phys_f, tv_f);
       while (k < ntile) {
-        compute_tile(s_lo + TILE * k, kA, vA);
+        compute_tile(s_lo + TILE * k, kA, vA, subA);
         k += wph;
-        if (k < ntile) load_tile(s_lo + TILE * k, kA, vA);
+        if (k < ntile) load_tile(s_lo + TILE * k, kA, vA, subA);
       }
     }
 
