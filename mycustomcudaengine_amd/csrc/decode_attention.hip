@@ -39,8 +39,9 @@
 //   fences, which on gfx950 write back the L2 per workgroup; the kernel
 //   boundary gives the same visibility for free.)
 //
-// Per wave and 16-token tile; a wave fetches its next tile once the current
-// one is computed.  One 8 KB tile in flight per wave (with a workgroup of 8
+// Per wave and 16-token tile; a wave issues its next tile's loads once the
+// current tile's scores are computed, so they land while its P V runs.  One 8
+// KB tile in flight per wave (with a workgroup of 8
 // waves on every CU, ~16 MB across the chip) covers the memory latency and
 // streams faster than more: 32-token tiles, or a second tile in flight per
 // wave, measured slower, and 8-token tiles slower again:
@@ -414,8 +415,11 @@ void paged_decode_kernel(DecodeArgs a) {
       // ---- loads of one tile: lane group lg owns tokens t0 + TPG lg .. + TPG - 1
       // (one block, since bs >= 8); each K and V row is one 256-byte run read by
       // 16 lanes x 16 bytes ----
-      auto load_rows = [&](int64_t phys, int tv, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG]) {
-        const int64_t off = ((phys << bs_log2) + (tv & (bs - 1))) * slot_stride + lr * 8;
+      auto load_rows = [&](int phys, int tv, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG]) {
+        // the token's slot in the pool: below 2^32 (checked on the host), so
+        // one 32 x 32 -> 64-bit multiply-add gives the element offset
+        const uint32_t slot = ((uint32_t)phys << bs_log2) + (uint32_t)(tv & (bs - 1));
+        const int64_t off = (int64_t)((uint64_t)slot * (uint32_t)slot_stride) + lr * 8;
 #pragma unroll
         for (int s8 = 0; s8 < TPG; ++s8) kk[s8] = ld_nt(kbase + off + s8 * slot_stride);
 #pragma unroll
@@ -459,8 +463,10 @@ void paged_decode_kernel(DecodeArgs a) {
         lds_barrier();
       }
       if (!active) continue;
-      // ---- compute of one tile ----
-      auto tile_body = [&](int t0, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG]) {
+      // ---- compute of one tile, in two parts: scores and softmax (p packed
+      // into pp), then P V ----
+      using Pk = uint32_t[TPG / 2][G];
+      auto tile_scores = [&](int t0, u32x4 (&kk)[TPG], Pk &pp) {
         const int tv = t0 + TPG * lg;
         // the tile reaches the end of the range (wave-uniform): only such a
         // tile masks tokens
@@ -505,7 +511,6 @@ void paged_decode_kernel(DecodeArgs a) {
         // row sum is taken from the same packed values (v_dot2 against 1.0),
         // so numerator and denominator use the one rounded p
         const uint32_t ones = T::pack_p(1.0f, 1.0f);
-        uint32_t pp[TPG / 2][G];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
           // (s - m) c rather than one FMA: exactly 0 at the max, so a single
@@ -525,6 +530,10 @@ void paged_decode_kernel(DecodeArgs a) {
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[h][e] *= alpha[h];
         }
+      };
+      auto tile_pv = [&](int t0, u32x4 (&vv)[TPG], const Pk &pp) {
+        const int tv = t0 + TPG * lg;
+        const bool tail = t0 + TILE > t_end;
         // tokens past the end: zero their V rows (p is 0, V may be NaN garbage)
         if (tail) {
 #pragma unroll
@@ -552,7 +561,7 @@ void paged_decode_kernel(DecodeArgs a) {
       // the slot is patched, in place, every row by a select (a conditional
       // write of one row would become an indexed register write, which puts
       // the tile in scratch memory).
-      auto compute_tile = [&](int t0, u32x4 (&kk)[TPG], u32x4 (&vv)[TPG], const int sub) {
+      auto patch_tile = [&](u32x4 (&kk)[TPG], u32x4 (&vv)[TPG], const int sub) {
         if (FUSED && __builtin_expect(__ballot(sub >= 0) != 0, 0)) {
           const u32x4 kn = knv_lds[lr], vn = knv_lds[16 + lr];
 #pragma unroll
@@ -565,10 +574,11 @@ void paged_decode_kernel(DecodeArgs a) {
             }
           }
         }
-        tile_body(t0, kk, vv);
       };
 
-      // ---- tile loop: compute the tile in registers, then fetch the wave's next ----
+      // ---- tile loop: the next tile's loads leave once the current tile's
+      // scores are done, and land while its P V runs (one query head per
+      // wave: the tiles alternate between two register sets) ----
       int subA = -1;  // patch row of the tile in kA / vA
       if (!FUSED && a.per_seq && k < ntile) load_tile(s_lo + TILE * k, kA, vA, subA);
       if constexpr (FUSED) {
@@ -595,10 +605,33 @@ void paged_decode_kernel(DecodeArgs a) {
         lds_barrier();
       }
       if constexpr (FUSED) subA = patch_row(phys_f, tv_f);
-      while (k < ntile) {
-        compute_tile(s_lo + TILE * k, kA, vA, subA);
-        k += wph;
-        if (k < ntile) load_tile(s_lo + TILE * k, kA, vA, subA);
+      Pk pp;
+      if constexpr (G == 1) {
+        u32x4 kB[TPG], vB[TPG];
+        int subB = -1;
+        while (k < ntile) {
+          patch_tile(kA, vA, subA);
+          tile_scores(s_lo + TILE * k, kA, pp);
+          const int kn = k + wph;
+          if (kn < ntile) load_tile(s_lo + TILE * kn, kB, vB, subB);
+          tile_pv(s_lo + TILE * k, vA, pp);
+          if (kn >= ntile) break;
+          patch_tile(kB, vB, subB);
+          tile_scores(s_lo + TILE * kn, kB, pp);
+          k = kn + wph;
+          if (k < ntile) load_tile(s_lo + TILE * k, kA, vA, subA);
+          tile_pv(s_lo + TILE * kn, vB, pp);
+        }
+      } else {
+        // (more query heads per wave: one register set measured faster; the
+        // compiler keeps the tile's V rows in copies while the next loads land)
+        while (k < ntile) {
+          patch_tile(kA, vA, subA);
+          tile_scores(s_lo + TILE * k, kA, pp);
+          tile_pv(s_lo + TILE * k, vA, pp);
+          k += wph;
+          if (k < ntile) load_tile(s_lo + TILE * k, kA, vA, subA);
+        }
       }
     }
 
@@ -843,6 +876,8 @@ int decode_impl(int dtype, const void *query, const void *key_cache, const void 
               block_size);
   MCE_REQUIRE(max_blocks_per_seq >= 1, "mce_paged_attention_decode: max_blocks_per_seq must be >= 1");
   MCE_REQUIRE(num_blocks >= 1, "mce_paged_attention_decode: empty KV pool");
+  MCE_REQUIRE(num_blocks <= ((int64_t)1 << 32) / block_size,
+              "mce_paged_attention_decode: KV pool above 2^32 token slots");
   MCE_REQUIRE((int64_t)max_blocks_per_seq * block_size <= ((int64_t)1 << 26),
               "mce_paged_attention_decode: context capacity above 2^26 tokens");
   if (batch == 0) return MCE_OK;
