@@ -113,6 +113,15 @@ struct DecodeArgs {
 
 __device__ inline int clamp_ctx(int c, int cap) { return c < 0 ? 0 : (c > cap ? cap : c); }
 
+// One stage of row16_sum applied to every value of v.
+template <int CTRL, int N, int M>
+__device__ __forceinline__ void row16_sum_stage(float (&v)[N][M]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+#pragma unroll
+    for (int j = 0; j < M; ++j) v[i][j] += dpp_f<CTRL>(v[i][j]);
+}
+
 // Exclusive prefix sum of per-sequence split weights (tiles + SEG_TILES for a
 // non-empty sequence) into pre[0..B], and the clamped context lengths into
 // ctx_out[0..B) (so the segments do not load them again); returns NT.  Sequence b's real tiles
@@ -484,8 +493,15 @@ void paged_decode_kernel(DecodeArgs a) {
               // (explicit conversions: bit_cast of an ext-vector element picks
               // element 0 in this compiler)
               d = T::dot2((uint32_t)kk[s8][k], (uint32_t)qv[h][k], d);
-            sc[s8][h] = row16_sum(d);
+            sc[s8][h] = d;
           }
+        // the 16-lane sums (row16_sum), one DPP stage at a time across all
+        // TPG G values: the chains interleave instead of waiting out each
+        // other's DPP read-after-write hazards
+        row16_sum_stage<0xB1>(sc);
+        row16_sum_stage<0x4E>(sc);
+        row16_sum_stage<0x141>(sc);
+        row16_sum_stage<0x140>(sc);
         if (tail) {
 #pragma unroll
           for (int s8 = 0; s8 < TPG; ++s8)
