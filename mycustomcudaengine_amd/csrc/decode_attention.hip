@@ -515,10 +515,10 @@ void paged_decode_kernel(DecodeArgs a) {
         for (int h = 0; h < G; ++h) {
           float mx = sc[0][h];
 #pragma unroll
-          for (int s8 = 1; s8 < TPG; ++s8) mx = fmaxf(mx, sc[s8][h]);
+          for (int s8 = 1; s8 < TPG; ++s8) mx = max_nq(mx, sc[s8][h]);
           mx = xor32_max(xor16_max(mx));
           mx = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, mx)));
-          const float mn = fmaxf(m_run[h], mx);
+          const float mn = max_nq(m_run[h], mx);
           alpha[h] = fast_exp2((m_run[h] - mn) * c);
           rescale |= mn != m_run[h];
           m_run[h] = mn;

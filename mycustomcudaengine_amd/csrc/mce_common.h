@@ -122,11 +122,21 @@ __device__ inline float dpp_f(float v) {
                                          0xf, 0xf, false));
 }
 
+// max(a, b) as med3(a, b, FLT_MAX): one v_med3_f32.  fmaxf in IEEE mode first
+// quiets signalling NaNs, a v_max_f32 x, x, x per operand the compiler cannot
+// prove canonical (DPP, permlane and select results); a med3 with +inf is
+// folded back into that max.  The maxima here are of scores and running
+// maxima, finite or -inf (never +inf); a NaN operand gives an unspecified
+// one of the two.
+__device__ __forceinline__ float max_nq(float a, float b) {
+  return __builtin_amdgcn_fmed3f(a, b, 3.402823466e+38f);
+}
+
 __device__ inline float row16_max(float v) {
-  v = fmaxf(v, dpp_f<0xB1>(v));
-  v = fmaxf(v, dpp_f<0x4E>(v));
-  v = fmaxf(v, dpp_f<0x141>(v));
-  v = fmaxf(v, dpp_f<0x140>(v));
+  v = max_nq(v, dpp_f<0xB1>(v));
+  v = max_nq(v, dpp_f<0x4E>(v));
+  v = max_nq(v, dpp_f<0x141>(v));
+  v = max_nq(v, dpp_f<0x140>(v));
   return v;
 }
 
@@ -148,7 +158,7 @@ __device__ inline float row16_sum(float v) {
 __device__ __forceinline__ float xor16_max(float x) {
   const unsigned u = __builtin_bit_cast(unsigned, x);
   const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+  return max_nq(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
 }
 __device__ __forceinline__ float xor16_add(float x) {
   const unsigned u = __builtin_bit_cast(unsigned, x);
@@ -158,7 +168,7 @@ __device__ __forceinline__ float xor16_add(float x) {
 __device__ __forceinline__ float xor32_max(float x) {
   const unsigned u = __builtin_bit_cast(unsigned, x);
   const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+  return max_nq(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
 }
 __device__ __forceinline__ float xor32_add(float x) {
   const unsigned u = __builtin_bit_cast(unsigned, x);
