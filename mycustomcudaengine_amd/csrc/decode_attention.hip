@@ -652,16 +652,20 @@ void paged_decode_kernel(DecodeArgs a) {
     }
 
     // ---- per-wave reduction over the four lane groups ----
+    // (one exchange stage at a time across all values, so the exchanges of
+    // different values interleave)
     float l_tot[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float v = l_grp[h];
-      l_tot[h] = xor32_add(xor16_add(v));
+      l_tot[h] = xor16_add(l_grp[h]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float x = acc[h][e];
-        acc[h][e] = xor32_add(xor16_add(x));
-      }
+      for (int e = 0; e < 8; ++e) acc[h][e] = xor16_add(acc[h][e]);
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      l_tot[h] = xor32_add(l_tot[h]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] = xor32_add(acc[h][e]);
     }
     const int64_t row0 = (int64_t)b * a.Hq + head0;
     const int slot = j + b;  // this piece's partial slot (compact layout)
