@@ -120,7 +120,8 @@ MCE_API size_t mce_paged_attention_decode_workspace_size(int batch, int num_head
  * max_blocks_per_seq * block_size; block ids outside [0, num_blocks) are
  * clamped into range (the reference reads out of bounds there).
  * head_dim must be 128, block_size a power of two in [8, 256],
- * num_heads / num_kv_heads in [1, 8].
+ * num_heads / num_kv_heads in [1, 8], num_blocks * block_size <= 2^32
+ * token slots.
  * Workspace: 256-byte aligned, at least
  * mce_paged_attention_decode_workspace_size() bytes, no initialisation
  * needed; it is scratch for the duration of the call (two calls that run

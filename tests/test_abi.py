@@ -98,6 +98,9 @@ def test_decode_validation(lib):
     assert _decode(lib, dtype=1) == _lib.MCE_ERR_WORKSPACE  # bf16 is supported
     assert _decode(lib, q=None) == _lib.MCE_ERR_INVALID
     assert _decode(lib, nb=0) == _lib.MCE_ERR_INVALID
+    # the pool is addressed by 32-bit token slots
+    assert _decode(lib, nb=(1 << 28) + 1) == _lib.MCE_ERR_INVALID and "2^32" in _err(lib)
+    assert _decode(lib, nb=1 << 28) == _lib.MCE_ERR_WORKSPACE  # 2^32 slots: accepted
     assert _decode(lib) == _lib.MCE_ERR_WORKSPACE  # no workspace given
     assert _decode(lib, B=0) == _lib.MCE_OK
 
