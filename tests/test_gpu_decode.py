@@ -266,8 +266,10 @@ def test_fused_rope_decode_equals_separate_ops(dev, hq, hkv, b):
     """decode_rope_attention (RoPE + KV append + attention in one launch) is
     bit-identical to rope_kv_store(query_out=...) + paged_attention_decode:
     output, key cache and value cache.  q/k/v are views into one fused
-    projection row; one position lies outside the RoPE table (not rotated)
-    and one slot is -1 (no store), as the separate ops treat them."""
+    projection row; one position lies outside the RoPE table (not rotated),
+    one slot is -1 (no store) and one lies at an earlier position of its
+    sequence (the row the attention reads there is the new one), as the
+    separate ops treat them."""
     d, bs, mb, rows = 128, 16, 40, 700
     gen = torch.Generator().manual_seed(hq * 31 + b)
     ctx = torch.randint(1, mb * bs + 1, (b,), generator=gen).tolist()
@@ -279,6 +281,9 @@ def test_fused_rope_decode_equals_separate_ops(dev, hq, hkv, b):
     if b > 2:
         slots[1] = -1
         pos[2] = rows + 5  # outside the table
+    if b > 3 and ctx[3] > 1:
+        p3 = ctx[3] // 2  # an earlier token of sequence 3 takes the new k / v
+        slots[3] = int(bt[3, p3 // bs]) * bs + p3 % bs
     inv = 1.0 / (500000.0 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
     ang = torch.outer(torch.arange(rows, dtype=torch.float32), inv)
     cos, sin = ang.cos().contiguous(), ang.sin().contiguous()
