@@ -407,7 +407,9 @@ def bench_prefill_vs_sdpa(dev, steps: int) -> list:
     24 / 8 heads, D=128, fp16 ~ N(0, 1), S = 128 .. 2048; prefill_attention timed beside
     torch.nn.functional.scaled_dot_product_attention(is_causal=True) on the K/V
     repeat-interleaved to 24 heads (its comparison), both with HIP events over back-to-back
-    calls after MFMA_WARMUP_CALLS warm-up calls; TFLOP/s over the causal pairs."""
+    calls after MFMA_WARMUP_CALLS warm-up calls; TFLOP/s over the causal pairs.  At small S
+    an eager Python call outlasts the kernel, so both are also timed as 20-call hipGraphs
+    (`graph_us`, `sdpa_graph_us`): the kernels' own time per call."""
     import my_cuda_engine_cpp as ops
     from torch.nn.attention import SDPBackend, sdpa_kernel
     rows = []
@@ -422,6 +424,8 @@ def bench_prefill_vs_sdpa(dev, steps: int) -> list:
                       rounds=3)
         row = {"seq_len": s, "us": round(ms * 1e3, 2),
                "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+        gms = time_graph_batch(lambda: ops.prefill_attention(q, k, v, scale))
+        row["graph_us"] = round(gms * 1e3, 2)
         qh = q.transpose(1, 2).contiguous()
         kh = k.transpose(1, 2).repeat_interleave(3, dim=1).contiguous()
         vh = v.transpose(1, 2).repeat_interleave(3, dim=1).contiguous()
@@ -432,11 +436,20 @@ def bench_prefill_vs_sdpa(dev, steps: int) -> list:
                     qh, kh, vh, is_causal=True, scale=scale), steps, MFMA_WARMUP_CALLS, rounds=3)
             row["sdpa_us"] = round(sms * 1e3, 2)
             row["speedup_vs_sdpa"] = round(sms / ms, 2)
+            try:
+                with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                    sgms = time_graph_batch(lambda: torch.nn.functional.scaled_dot_product_attention(
+                        qh, kh, vh, is_causal=True, scale=scale))
+                row["sdpa_graph_us"] = round(sgms * 1e3, 2)
+                row["speedup_vs_sdpa_graph"] = round(sgms / gms, 2)
+            except RuntimeError as e:  # SDPA refused capture
+                row["sdpa_graph_error"] = str(e)[:200]
         except RuntimeError as e:  # no fused SDPA backend on this build
             row["sdpa_us"] = None
             row["sdpa_error"] = str(e)[:200]
         rows.append(row)
-        log(f"prefill S={s}: {row['us']} us ({row['tflops']} TFLOP/s); SDPA {row.get('sdpa_us')} us")
+        log(f"prefill S={s}: {row['us']} us ({row['tflops']} TFLOP/s), {row['graph_us']} us in a graph; "
+            f"SDPA {row.get('sdpa_us')} us, {row.get('sdpa_graph_us')} us in a graph")
     return rows
 
 
