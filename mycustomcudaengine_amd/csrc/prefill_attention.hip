@@ -806,8 +806,11 @@ void prefill_causal_kernel(PrefillArgs a) {
       const int grow = r_wave + rr;
       if (grow < rows_total) {
         const int p = grow / G, hh = g * G + (grow - p * G);
-        *reinterpret_cast<u32x4 *>(a.out + ((int64_t)b * S + p) * q_row_stride +
-                                   (int64_t)hh * PF_HD + dim0 + 8 * ch) = val;
+        // non-temporal: the output is not read again by this kernel
+        // (back-to-back cfg3 calls 35.2 -> 34.8 us, S = 1024 -2.5 %)
+        __builtin_nontemporal_store(val, reinterpret_cast<u32x4 *>(
+                                             a.out + ((int64_t)b * S + p) * q_row_stride +
+                                             (int64_t)hh * PF_HD + dim0 + 8 * ch));
       }
     }
   }  // items of this workgroup
