@@ -1,6 +1,8 @@
 // Error reporting and version entry points of libmce.so.
 #include "mce_common.h"
 
+#include <atomic>
+
 namespace mce {
 
 static thread_local char g_last_error[512] = {0};
@@ -23,18 +25,20 @@ int check_launch(const char *what) {
   return MCE_OK;
 }
 
+// CUs of the current device, looked up once per device (threads that race
+// on the first lookup store the same value)
 int cu_count() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    cached[dev] = n;
+    cached[dev].store(n, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return n;
 }
 
 }  // namespace mce
