@@ -214,6 +214,7 @@ void prefill_causal_kernel(PrefillArgs a) {
   // epilogue reuses them all.  The other launches load Q straight into
   // registers: their LDS has to leave room for two workgroups per CU.
   constexpr bool Q_LDS = KSPLIT == 2 && NRB == 4;
+  constexpr bool PRIO_A = KSPLIT == 2 && !Q_LDS;  // the small-grid launch
   constexpr int TILE_HALFS = (2 * KSPLIT * 2 * TILE + (Q_LDS ? NRB * PF_TILE : 0)) / 2;
   constexpr int LDS_HALFS = TILE_HALFS > EPI_HALFS ? TILE_HALFS : EPI_HALFS;
   __shared__ __attribute__((aligned(16))) uint16_t lds[LDS_HALFS];
@@ -589,6 +590,12 @@ void prefill_causal_kernel(PrefillArgs a) {
       // block (same instructions, another order): 1-2% faster at every shape
       // measured, with fewer registers.
       __builtin_amdgcn_iglp_opt(0);
+      // Small-grid launch (two 4-wave workgroups per CU, so each SIMD runs
+      // waves of two workgroups, not held in one phase by a common barrier):
+      // the score phase issues at raised wave priority, back to normal for
+      // P V.  B=1 S=128 / 256 / 512 in 20-call graphs 2 / 3 / 4 % faster; on
+      // the 8-wave and one-stream launches it measured neutral to 2 % slower.
+      if constexpr (PRIO_A) __builtin_amdgcn_s_setprio(1);
       const int kt = tb + KSPLIT * u + kh;  // key tile
       const char *kb = ks_h + ((u + 1) & 1) * TILE;
       const char *vb = vs_h + (u & 1) * TILE;
@@ -623,6 +630,7 @@ void prefill_causal_kernel(PrefillArgs a) {
           l_i = T::dot2(pp, ones, l_i);
           pk[hh][e2 >> 2][e2 & 3] = pp;
         }
+      if constexpr (PRIO_A) __builtin_amdgcn_s_setprio(0);
       // ---- B: P V of tile u while tile u + 1 is masked and max-reduced
 #pragma unroll
       for (int hh = 0; hh < NH; ++hh) {
